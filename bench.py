@@ -1,0 +1,209 @@
+#!/usr/bin/env python3
+"""Benchmark: FlashAttention forward on one MI355X.
+
+One "step" is one forward call (O plus the fp32 row LSE) over the headline
+workload, B4 H32 S2048 D128 bf16 causal, with q/k/v already resident in HBM.
+Prints ONE JSON line on stdout:
+
+  value        whole-job TFLOP/s = 4*B*H*S*S*D/2 / (wall time per step)
+  roofline     the kernel's TFLOP/s from HIP events on the launch stream,
+               against MI355X's dense bf16 MFMA peak (2516.6 TFLOP/s)
+  cpu_baseline the CPU oracle (numpy fp32 formula) timed on this host's
+               cores over a bounded sample of the same workload (whole heads)
+
+Everything else (per-call evaluator-style wall clock, the run's sizes) goes to
+stderr.  Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+METRIC = "attn fwd TFLOP/s + % bf16 MFMA peak, B4·H32·S2048·D128 causal, 1 GPU"
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16/fp16 MFMA: 256 CU x 4096 FLOP/clk x 2.4 GHz
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def read_traffic(workload_tag: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc, if a summary exists.
+
+    profiles/<tag>_traffic.txt holds lines `fetch_bytes=<int>` and
+    `write_bytes=<int>` (per dispatch, already scaled by the copy-kernel
+    calibration factor recorded in the same file).
+    """
+    path = REPO / "profiles" / f"{workload_tag}_traffic.txt"
+    if not path.exists():
+        return None
+    vals = {}
+    for line in path.read_text().splitlines():
+        if "=" in line and not line.lstrip().startswith("#"):
+            k, v = line.split("=", 1)
+            vals[k.strip()] = v.strip()
+    try:
+        return int(vals["fetch_bytes"]) + int(vals["write_bytes"])
+    except (KeyError, ValueError):
+        return None
+
+
+def cpu_baseline(w, budget_s: float):
+    """Time the CPU oracle on whole heads of the workload until ~budget_s."""
+    import numpy as np
+    import torch
+    from oracle.attention_oracle import attention_ref
+
+    threads = len(os.sched_getaffinity(0))
+    try:
+        from threadpoolctl import threadpool_limits
+        limiter = threadpool_limits(limits=threads)
+    except Exception:  # noqa: BLE001
+        limiter = None
+    from flash_attn_npu_amd.workloads import make_inputs
+    q, k, v = make_inputs(w, device=None, batch_slice=slice(0, 1))
+    qn, kn, vn = (t.float().numpy() for t in (q, k, v))
+    # one warm-up head
+    attention_ref(qn[0, 0], kn[0, 0], vn[0, 0], w.causal, w.sm_scale, out_dtype="bfloat16")
+    heads = 0
+    t0 = time.perf_counter()
+    while heads < w.H and time.perf_counter() - t0 < budget_s:
+        attention_ref(qn[0, heads], kn[0, heads], vn[0, heads], w.causal, w.sm_scale,
+                      out_dtype="bfloat16")
+        heads += 1
+    elapsed = time.perf_counter() - t0
+    if limiter is not None:
+        limiter.restore_original_limits()
+    flops = 4.0 * heads * w.S * w.S * w.D / (2.0 if w.causal else 1.0)
+    try:
+        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except Exception:  # noqa: BLE001
+        model = "unknown"
+    return {
+        "value": flops / elapsed / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{heads} of {w.B * w.H} (b,h) heads of the same workload (b=0), full S={w.S} "
+                  f"rows each, numpy fp32 oracle, {elapsed:.1f} s, charged the same causal-halved "
+                  f"FLOP formula; CPU: {model}",
+        "seconds_per_step_extrapolated": elapsed * (w.B * w.H) / max(heads, 1),
+    }
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, help="1-based index of the measured configuration")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget (0 = skip)")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported "
+              "(this forward needs no collective; heads shard across GPUs with no exchange).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    from flash_attn_npu_amd import flash_attention_forward as fa
+    from flash_attn_npu_amd.workloads import CONFIGS, make_inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    fa._load_library()
+    w = CONFIGS[args.config - 1]
+    log(f"workload: {w.describe()} sm_scale={w.sm_scale:.6f}")
+    q, k, v = make_inputs(w, device="cuda")
+    torch.cuda.synchronize()
+    rt = fa._describe_runtime(w.B, w.H, w.S, w.D, w.causal)
+    log(f"runtime: {rt}")
+
+    def step():
+        return fa.attention(q, k, v, w.causal, w.sm_scale, return_lse=w.with_lse)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = ev0.elapsed_time(ev1)
+
+    # Evaluator-style per-call wall clock (perf_counter around call + synchronize,
+    # evaluate_attention.py:233-264), for comparison only.
+    samples = []
+    for _ in range(20):
+        s0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        samples.append((time.perf_counter() - s0) * 1e6)
+
+    ms_per_step = wall * 1e3 / args.steps
+    kernel_ms = ev_ms / args.steps
+    value = w.flops / (ms_per_step * 1e-3) / 1e12
+    achieved = w.flops / (kernel_ms * 1e-3) / 1e12
+    log(f"wall {ms_per_step * 1e3:.1f} us/step, events {kernel_ms * 1e3:.1f} us/launch, "
+        f"evaluator-style median {statistics.median(samples):.1f} us")
+    log(f"HBM-level algorithmic bytes {w.io_bytes} -> {w.io_bytes / (kernel_ms * 1e-3) / 1e9:.0f} GB/s")
+
+    tag = w.name
+    traffic = read_traffic(tag)
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "pct_of_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w.dtype == torch.bfloat16 else "fp16",
+        "data": "synthetic (seeded N(0,1) q/k/v, CPU generator)",
+        "config": {"workload": f"attn fwd {tag}", "B": w.B, "H": w.H, "S": w.S, "D": w.D,
+                   "causal": w.causal, "sm_scale": w.sm_scale, "lse": w.with_lse,
+                   "BLOCK_M": rt["selected_config"]["BLOCK_M"], "BLOCK_N": rt["selected_config"]["BLOCK_N"],
+                   "waves": rt["waves"], "grid": rt["launched_programs"]},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic, "kernel_us": round(kernel_ms * 1e3, 2),
+                     "algorithmic_flops": w.flops, "algorithmic_bytes": w.io_bytes},
+        "evaluator_median_us": round(statistics.median(samples), 2),
+    }
+    if args.cpu_seconds > 0:
+        cb = cpu_baseline(w, args.cpu_seconds)
+        cb.pop("seconds_per_step_extrapolated", None)
+        result["cpu_baseline"] = cb
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,72 @@
+"""Build recipe for libfa_mi355x.so (the HIP kernels + C ABI) for gfx950.
+
+Plain `hipcc -shared -fPIC` on the one source file: no torch cpp_extension,
+no hipify, one code path.  The library lands next to this file so the
+in-tree loader (flash_attention_forward._load_library) finds it and it
+travels with the source tree.
+
+    python -m flash_attn_npu_amd.build          # or __graft_entry__.build()
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO_DIR = PKG_DIR.parent
+SRC = PKG_DIR / "csrc" / "fa_fwd.hip"
+INCLUDE_DIR = REPO_DIR / "include"
+LIB_NAME = "libfa_mi355x.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+OFFLOAD_ARCH = os.environ.get("FA_OFFLOAD_ARCH", "gfx950")
+
+
+def hipcc_path() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: install ROCm or set HIPCC")
+
+
+def compile_command(out: Path = LIB_PATH, extra: list[str] | None = None) -> list[str]:
+    return [
+        hipcc_path(),
+        f"--offload-arch={OFFLOAD_ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-shared",
+        "-fPIC",
+        # Keep packed-fp32 VALU forms (v_pk_{add,mul,fma}_f32) out of the device code.
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wno-unused-command-line-argument",
+        f"-I{INCLUDE_DIR}",
+        *(extra or []),
+        "-o", str(out),
+        str(SRC),
+    ]
+
+
+def build_library(verbose: bool = False) -> Path:
+    """Compile the library (always; a stale .so is replaced atomically)."""
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = compile_command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # The host pass warns that it does not know the packed-fp32 feature; drop that noise.
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build_library(verbose=True))

@@ -1,0 +1,631 @@
+// fa_fwd.hip -- FlashAttention forward for AMD Instinct MI355X (gfx950).
+//
+// One hand-written HIP kernel family plus the C ABI declared in
+// include/fa_fwd.h.  It computes, per (batch, head),
+//     O = softmax(sm_scale * Q K^T  [+ causal mask]) V,   LSE = logsumexp(...)
+// which is what the reference Triton kernel `_attn_fwd`
+// (flash_attention_forward.py:1037-1111, inner loop :648-757, epilogue
+// :1022-1033) computes on Ascend.  The work decomposition is gfx950-native:
+//
+//  * A workgroup owns BM = 32*NW query rows of one (b, h); each of its NW
+//    wave64s owns 32 of them.  K and V tiles of BN keys are streamed through
+//    double-buffered LDS; the next tile's global loads (128-bit) are in flight
+//    while the current tile is computed, so one barrier per tile suffices.
+//  * Both products run on v_mfma_f32_32x32x16_{bf16,f16} with fp32
+//    accumulation, in transposed form:  S^T = K Q^T  and  O^T = V^T P^T.
+//    In the 32x32 accumulator layout lane l holds column l%32, so every lane
+//    owns exactly one query: the row max / row sum of the online softmax are
+//    in-lane reductions plus one v_permlane32_swap, the rescale factor is a
+//    per-lane scalar, and P^T leaves the S^T accumulator already in the
+//    B-operand layout of the second MFMA (no LDS round trip for P).
+//  * V is written to LDS transposed (V^T, key order permuted to match the
+//    accumulator layout, XOR-swizzled 16-byte chunks) so that the A operand of
+//    O^T = V^T P^T is one conflict-free ds_read_b128 per lane.
+//  * Q stays in VGPRs for the whole tile loop.  sm_scale*log2(e) is applied in
+//    fp32 after the MFMA (exp2 path); Q is never pre-scaled or re-rounded.
+//  * The running max is always kept (numerically stable), with a lazy update:
+//    it only moves when a new row max exceeds it by more than 2^8, so the
+//    O/l rescale is skipped on most tiles.  Exact by shift invariance.
+//  * Causal: KV tiles beyond the workgroup's last query are never loaded,
+//    waves skip tiles above their own diagonal, and only tiles crossing the
+//    diagonal or the ragged key tail evaluate the mask.  Ragged query/key
+//    tails are zero-filled on load, masked to -inf, and never stored.
+//  * Grid: one workgroup per (b, h, m-tile); consecutive logical tiles are
+//    kept on one XCD (workgroups are dispatched round-robin over the 8 XCDs)
+//    so the m-tiles of a head share that XCD's L2, and causal tiles of a head
+//    run heaviest first.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "fa_fwd.h"
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+// The running max only moves when a row max exceeds it by more than this many
+// log2 units, so un-normalised probabilities stay <= 2^8 (safe in fp16/bf16).
+constexpr float kLazyMaxThreshold = 8.0f;
+constexpr int kNumXcd = 8;
+constexpr int kMaxBlockM = 256;  // largest BLOCK_M of any kernel instance
+
+struct KernelArgs {
+  const char *q;
+  const char *k;
+  const char *v;
+  char *o;
+  float *lse;
+  int64_t q_sb, q_sh, q_ss;  // element strides (dim stride is 1)
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int32_t B, H, Sq, Sk;
+  int32_t n_mtiles;     // ceil(Sq / BM)
+  int32_t total_tiles;  // n_mtiles * B * H
+  int32_t xcd_remap;    // 1: grid == total_tiles, keep logical neighbours on one XCD
+  uint32_t q_sign;      // 0x80008000 when sm_scale < 0 (Q is negated in registers)
+  float c;              // |sm_scale| * log2(e), > 0
+};
+
+template <bool BF16>
+__device__ __forceinline__ f32x16_t mfma32x32x16(u32x4_t a, u32x4_t b, f32x16_t c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+// Two fp32 -> one dword of two 16-bit values (round to nearest even);
+// a single v_cvt_pk_{bf16,f16}_f32 on gfx950.
+template <bool BF16>
+__device__ __forceinline__ uint32_t pack2(float x, float y) {
+  f32x2_t v = {x, y};
+  if constexpr (BF16) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
+  }
+}
+
+// Combine a value across the two lane halves (lane l and lane l^32) with one
+// v_permlane32_swap.  The instruction swaps the upper 32 lanes of its first
+// operand with the lower 32 lanes of its second; with both operands equal to x
+// each lane ends up holding its own value in one result and its partner's in
+// the other, so a symmetric op over the two results is the 2-lane reduction.
+__device__ __forceinline__ float halves_max(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Buffer resources: one scalar descriptor per (b, h) tensor slice.  Loads
+// outside [0, num_records) return zero and stores there are dropped, which is
+// how ragged query/key tails are handled without branches.
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+constexpr int kBufferFlags = 0x00020000;  // gfx9 dword3: 32-bit data format, no swizzle
+
+__device__ __forceinline__ BufRsrc make_rsrc(const void *base, uint32_t num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)num_bytes,
+                                           kBufferFlags);
+}
+__device__ __forceinline__ u32x4_t buf_load16(BufRsrc r, uint32_t voff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+__device__ __forceinline__ void buf_store8(u32x2_t v, BufRsrc r, uint32_t voff) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, voff, 0, 0);
+}
+__device__ __forceinline__ void buf_store4(uint32_t v, BufRsrc r, uint32_t voff) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, voff, 0, 0);
+}
+
+// Position of key `k` (0..BN-1) inside a V^T row in LDS.  In each group of 16
+// keys, the 4-key groups 1 and 2 trade places.  This is the order in which a
+// lane's S^T accumulator registers reach the B operand of the P*V MFMA: lane
+// (h, n) holds keys 8j + 4h + i of a 32-key block in register 4j + i, and
+// feeds registers 8t..8t+7 as k-indices 8h..8h+7 of k-step t.
+__device__ __forceinline__ int vt_pos(int k) {
+  int g = (k >> 2) & 3;
+  int pg = (g == 1) ? 2 : (g == 2 ? 1 : g);
+  return (k & ~15) | (pg << 2) | (k & 3);
+}
+
+// Logical tile index for workgroup `bid`.  When every tile has its own
+// workgroup, workgroups are dealt round-robin to the XCDs; renumber them so
+// that each XCD receives one contiguous run of logical tiles.
+__device__ __forceinline__ int logical_tile(int bid, int grid, int remap) {
+  if (!remap) return bid;
+  int x = bid % kNumXcd;
+  int base = grid / kNumXcd;
+  int extra = grid % kNumXcd;
+  // XCDs [0, extra) get base+1 workgroups, the rest get base.
+  int prefix = x * base + (x < extra ? x : extra);
+  return prefix + bid / kNumXcd;
+}
+
+template <int D, int BN, int NW, bool BF16, bool CAUSAL>
+struct FaConfig {
+  static constexpr int BM = 32 * NW;           // query rows per workgroup
+  static constexpr int NT = 64 * NW;           // threads per workgroup
+  static constexpr int DCH = D / 8;            // 16-byte chunks per K/V row
+  static constexpr int NKG = NT / DCH;         // key groups loaded per pass
+  static constexpr int CPT = BN / NKG;         // keys per thread per tile
+  static constexpr int RK = D * 2 + 16;        // LDS bytes per K row (padded)
+  static constexpr int RV = BN * 2 + 16;       // LDS bytes per V^T row (padded)
+  static constexpr int NCH = BN / 8;           // 16-byte chunks per V^T row
+  static constexpr int K_BYTES = BN * RK;
+  static constexpr int V_BYTES = D * RV;
+  static constexpr int STAGE_BYTES = K_BYTES + V_BYTES;
+  static constexpr int LDS_BYTES = 2 * STAGE_BYTES;
+  static_assert(D % 32 == 0, "head dim must be a multiple of 32");
+  static_assert(BN % 32 == 0, "BN must be a multiple of 32");
+  static_assert(NT % DCH == 0, "threads must tile the chunk columns");
+  static_assert(NKG * CPT == BN && CPT >= 1 && CPT <= 4 && (4 % CPT) == 0,
+                "each thread loads 1, 2 or 4 keys of one 4-key group");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one gfx950 CU");
+};
+
+template <int D, int BN, int NW, bool BF16, bool CAUSAL>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+fa_fwd_kernel(KernelArgs p) {
+  using C = FaConfig<D, BN, NW, BF16, CAUSAL>;
+  constexpr int BM = C::BM;
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31;   // query column of this lane (and MFMA A-operand row)
+  const int h = lane >> 5;   // lane half
+
+  // Loader mapping: thread -> (16-byte column chunk, group of CPT keys).
+  const int ld_dc = tid % C::DCH;
+  const int ld_kg = tid / C::DCH;
+  // Byte offsets of this thread's CPT rows inside a K/V tile (tile-invariant).
+  uint32_t koff[C::CPT], voff[C::CPT];
+#pragma unroll
+  for (int j = 0; j < C::CPT; ++j) {
+    koff[j] = (uint32_t)((ld_kg * C::CPT + j) * p.k_ss * 2 + 16 * ld_dc);
+    voff[j] = (uint32_t)((ld_kg * C::CPT + j) * p.v_ss * 2 + 16 * ld_dc);
+  }
+  // LDS byte offsets (within a stage) written by this thread.
+  const uint32_t k_wr = (uint32_t)((ld_kg * C::CPT) * C::RK + 16 * ld_dc);
+  const int pos0 = vt_pos(ld_kg * C::CPT);
+  const uint32_t v_wr = (uint32_t)(C::K_BYTES + (8 * ld_dc) * C::RV +
+                                   (((pos0 >> 3) ^ (ld_dc & (C::NCH - 1))) * 16) + (pos0 & 7) * 2);
+  // LDS byte offsets read by this lane for the A operands.
+  const uint32_t k_rd = (uint32_t)(n * C::RK + h * 16);
+
+  const float c = p.c;
+
+  for (int slot = blockIdx.x; slot < p.total_tiles; slot += gridDim.x) {
+    const int L = logical_tile(slot, gridDim.x, p.xcd_remap);
+    const int bh = L / p.n_mtiles;
+    const int mr = L - bh * p.n_mtiles;
+    const int mt = CAUSAL ? (p.n_mtiles - 1 - mr) : mr;  // causal: heaviest first
+    const int bb = bh / p.H;
+    const int hh = bh - bb * p.H;
+
+    const int q0 = mt * BM;
+    const int q0w = q0 + 32 * wave;
+    const int qrow = q0w + n;
+
+    const char *qg = p.q + 2 * (bb * p.q_sb + hh * p.q_sh);
+    const char *kg = p.k + 2 * (bb * p.k_sb + hh * p.k_sh);
+    const char *vg = p.v + 2 * (bb * p.v_sb + hh * p.v_sh);
+
+    // Q^T fragments (B operand of S^T = K Q^T): lane (h, n) holds
+    // Q[qrow][16s + 8h .. +8] for every 16-wide d-step s.  Rows >= Sq read 0.
+    u32x4_t qf[D / 16];
+    {
+      const BufRsrc rq = make_rsrc(qg, (uint32_t)((int64_t)p.Sq * p.q_ss * 2));
+      const uint32_t qo = (uint32_t)(qrow * p.q_ss * 2 + 16 * h);
+#pragma unroll
+      for (int s = 0; s < D / 16; ++s) qf[s] = buf_load16(rq, qo + 32 * s) ^ p.q_sign;
+    }
+
+    const int kv_end = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
+    const int n_tiles = (kv_end + BN - 1) / BN;
+    const int wave_last_q = q0w + 31;
+
+    u32x4_t kreg[C::CPT], vreg[C::CPT];
+    // Global -> registers for tile t; keys >= Sk fall outside the buffer
+    // range and read as zero.
+    auto gload = [&](int t) {
+      const int key0 = t * BN;
+      const BufRsrc rk = make_rsrc(kg + (int64_t)key0 * p.k_ss * 2,
+                                   (uint32_t)((int64_t)(p.Sk - key0) * p.k_ss * 2));
+      const BufRsrc rv = make_rsrc(vg + (int64_t)key0 * p.v_ss * 2,
+                                   (uint32_t)((int64_t)(p.Sk - key0) * p.v_ss * 2));
+#pragma unroll
+      for (int j = 0; j < C::CPT; ++j) {
+        kreg[j] = buf_load16(rk, koff[j]);
+        vreg[j] = buf_load16(rv, voff[j]);
+      }
+    };
+    // Registers -> LDS stage `buf`: K row-major, V transposed to V^T.
+    auto swrite = [&](int buf) {
+      char *st = smem + buf * C::STAGE_BYTES;
+#pragma unroll
+      for (int j = 0; j < C::CPT; ++j) *(u32x4_t *)(st + k_wr + j * C::RK) = kreg[j];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        char *dst = st + v_wr + i * C::RV;
+        const int w = i >> 1, sh = (i & 1) * 16;
+        if constexpr (C::CPT == 4) {
+          u32x2_t x;
+          x[0] = ((vreg[0][w] >> sh) & 0xffffu) | (((vreg[1][w] >> sh) & 0xffffu) << 16);
+          x[1] = ((vreg[2][w] >> sh) & 0xffffu) | (((vreg[3][w] >> sh) & 0xffffu) << 16);
+          *(u32x2_t *)dst = x;
+        } else if constexpr (C::CPT == 2) {
+          *(uint32_t *)dst = ((vreg[0][w] >> sh) & 0xffffu) | (((vreg[1][w] >> sh) & 0xffffu) << 16);
+        } else {
+          *(uint16_t *)dst = (uint16_t)((vreg[0][w] >> sh) & 0xffffu);
+        }
+      }
+    };
+
+    f32x16_t oacc[D / 32];
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) oacc[db] = (f32x16_t){};
+    float m_run = -INFINITY;  // running max, in scaled log2 units
+    float l_run = 0.f;        // this lane-half's partial row sum
+
+    if (n_tiles > 0) gload(0);
+    for (int t = 0; t < n_tiles; ++t) {
+      const int buf = t & 1;
+      swrite(buf);
+      __syncthreads();
+      if (t + 1 < n_tiles) gload(t + 1);
+
+      const int kbase = t * BN;
+      if (CAUSAL && kbase > wave_last_q) continue;  // whole tile above this wave's diagonal
+
+      const char *ks = smem + buf * C::STAGE_BYTES;
+      const char *vs = ks + C::K_BYTES;
+
+      // S^T = K Q^T: block kb covers keys kbase + 32kb .. +32.
+      f32x16_t sacc[BN / 32];
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb) {
+        sacc[kb] = (f32x16_t){};
+#pragma unroll
+        for (int s = 0; s < D / 16; ++s) {
+          const u32x4_t a = *(const u32x4_t *)(ks + k_rd + 32 * kb * C::RK + 32 * s);
+          sacc[kb] = mfma32x32x16<BF16>(a, qf[s], sacc[kb]);
+        }
+      }
+
+      // Mask only tiles crossing the diagonal or the ragged key tail.
+      const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && kbase + BN - 1 > q0w);
+      if (need_mask) {
+        // Register r of block kb holds key kbase + 4h + (32kb + 8(r>>2) + (r&3));
+        // it is visible iff that offset <= lim.
+        const int last_key = CAUSAL ? min(qrow, p.Sk - 1) : p.Sk - 1;
+        const int lim = last_key - kbase - 4 * h;
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int off = 32 * kb + 8 * (r >> 2) + (r & 3);
+            sacc[kb][r] = off <= lim ? sacc[kb][r] : -INFINITY;
+          }
+        }
+      }
+
+      // Online softmax for this lane's query.
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+      mx = halves_max(mx);
+      const float m_cand = mx * c;
+      const bool upd = m_cand > m_run + kLazyMaxThreshold;
+      const float m_new = upd ? m_cand : m_run;
+      if (__builtin_amdgcn_ballot_w64(upd)) {
+        const float alpha = upd ? fast_exp2(m_run - m_new) : 1.f;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) oacc[db] *= alpha;
+      }
+      m_run = m_new;
+      const float mb = (m_new == -INFINITY) ? 0.f : m_new;
+
+      float lsum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = fast_exp2(__builtin_fmaf(sacc[kb][r], c, -mb));
+          sacc[kb][r] = pv;
+          lsum[r & 3] += pv;
+        }
+      l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+
+      // P^T fragments: k-step ks (16 keys) = registers 8t..8t+7 of block ks/2.
+      u32x4_t pf[BN / 16];
+#pragma unroll
+      for (int ks2 = 0; ks2 < BN / 16; ++ks2) {
+        const int kb = ks2 >> 1, t8 = (ks2 & 1) * 8;
+        pf[ks2][0] = pack2<BF16>(sacc[kb][t8 + 0], sacc[kb][t8 + 1]);
+        pf[ks2][1] = pack2<BF16>(sacc[kb][t8 + 2], sacc[kb][t8 + 3]);
+        pf[ks2][2] = pack2<BF16>(sacc[kb][t8 + 4], sacc[kb][t8 + 5]);
+        pf[ks2][3] = pack2<BF16>(sacc[kb][t8 + 6], sacc[kb][t8 + 7]);
+      }
+
+      // O^T += V^T P^T: block db covers dims 32db .. +32.
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) {
+        const int d = 32 * db + n;
+        const char *vrow = vs + d * C::RV;
+        const int sw = (d >> 3) & (C::NCH - 1);
+#pragma unroll
+        for (int ks2 = 0; ks2 < BN / 16; ++ks2) {
+          const u32x4_t a = *(const u32x4_t *)(vrow + (((2 * ks2 + h) ^ sw) * 16));
+          oacc[db] = mfma32x32x16<BF16>(a, pf[ks2], oacc[db]);
+        }
+      }
+    }
+
+    // Epilogue: normalise, store O rows and the natural-log LSE.  Rows >= Sq
+    // fall outside the buffer range and their stores are dropped.
+    const float l_tot = halves_sum(l_run);
+    const float inv = 1.f / l_tot;
+    {
+      const char *og = p.o + 2 * (bb * p.o_sb + hh * p.o_sh);
+      const BufRsrc ro = make_rsrc(og, (uint32_t)((int64_t)p.Sq * p.o_ss * 2));
+      const uint32_t oo = (uint32_t)(qrow * p.o_ss * 2 + 8 * h);
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          u32x2_t x;
+          x[0] = pack2<BF16>(oacc[db][4 * j + 0] * inv, oacc[db][4 * j + 1] * inv);
+          x[1] = pack2<BF16>(oacc[db][4 * j + 2] * inv, oacc[db][4 * j + 3] * inv);
+          buf_store8(x, ro, oo + 2 * (32 * db + 8 * j));
+        }
+    }
+    if (p.lse != nullptr) {
+      const uint32_t nbytes = (uint32_t)p.Sq * 4u;
+      const BufRsrc rl = make_rsrc(p.lse + ((int64_t)bb * p.H + hh) * p.Sq, nbytes);
+      const float lse = (m_run + __log2f(l_tot)) * kLn2;
+      buf_store4(__builtin_bit_cast(uint32_t, lse), rl, h ? nbytes : (uint32_t)qrow * 4u);
+    }
+    if (slot + (int)gridDim.x < p.total_tiles) __syncthreads();  // LDS reuse by the next tile
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel table.
+typedef void (*KernelFn)(KernelArgs);
+
+struct KernelEntry {
+  int32_t D, dtype, causal, BN, NW;
+  int32_t lds_bytes;
+  KernelFn fn;
+};
+
+template <int D, int BN, int NW, bool BF16, bool CAUSAL>
+constexpr KernelEntry entry() {
+  return KernelEntry{D, BF16 ? 1 : 0, CAUSAL ? 1 : 0, BN, NW,
+                     FaConfig<D, BN, NW, BF16, CAUSAL>::LDS_BYTES,
+                     fa_fwd_kernel<D, BN, NW, BF16, CAUSAL>};
+}
+
+#define FA_ENTRIES_DT_C(D, BN, NW)                                                   \
+  entry<D, BN, NW, false, false>(), entry<D, BN, NW, false, true>(),                 \
+      entry<D, BN, NW, true, false>(), entry<D, BN, NW, true, true>()
+
+const KernelEntry kKernels[] = {
+    FA_ENTRIES_DT_C(64, 64, 4),
+    FA_ENTRIES_DT_C(128, 64, 4),
+};
+constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
+
+bool is_supported_head_dim(int d) { return d == 64 || d == 128; }
+
+// Default (BLOCK_N, waves) per head dim; BLOCK_M = 32 * waves.
+void default_tiling(int D, int dtype, int causal, int *bn, int *nw) {
+  (void)dtype;
+  (void)causal;
+  (void)D;
+  *bn = 64;
+  *nw = 4;
+}
+
+int find_kernel(int D, int dtype, int causal, int BN, int NW) {
+  for (int i = 0; i < kNumKernels; ++i) {
+    const KernelEntry &e = kKernels[i];
+    if (e.D == D && e.dtype == dtype && e.causal == causal && e.BN == BN && e.NW == NW) return i;
+  }
+  return -1;
+}
+
+struct Plan {
+  int kernel;
+  int BM, BN, NW;
+  int n_mtiles;
+  int64_t total_tiles;
+  int grid;
+};
+
+int make_plan(const fa_fwd_params *p, Plan *out) {
+  int bn, nw;
+  if (p->block_m == 0 && p->block_n == 0) {
+    default_tiling(p->D, p->dtype, p->causal, &bn, &nw);
+  } else {
+    if (p->block_m <= 0 || p->block_n <= 0 || p->block_m % 32 != 0) return FA_ERR_TILING;
+    bn = p->block_n;
+    nw = p->block_m / 32;
+  }
+  const int kid = find_kernel(p->D, p->dtype, p->causal ? 1 : 0, bn, nw);
+  if (kid < 0) return FA_ERR_TILING;
+  out->kernel = kid;
+  out->BN = bn;
+  out->NW = nw;
+  out->BM = 32 * nw;
+  out->n_mtiles = (p->Sq + out->BM - 1) / out->BM;
+  out->total_tiles = (int64_t)out->n_mtiles * p->B * p->H;
+  if (out->total_tiles > INT32_MAX) return FA_ERR_SHAPE;
+  int64_t grid = out->total_tiles;
+  if (p->num_programs > 0 && p->num_programs < grid) grid = p->num_programs;
+  out->grid = (int)grid;
+  return FA_OK;
+}
+
+bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int fa_abi_version(void) { return FA_ABI_VERSION; }
+
+const char *fa_error_string(int code) {
+  switch (code) {
+    case FA_OK: return "ok";
+    case FA_ERR_NULL: return "a required tensor pointer is NULL";
+    case FA_ERR_SHAPE: return "invalid shape (negative size, Sq>0 with Sk==0, or too many tiles)";
+    case FA_ERR_HEAD_DIM: return "HEAD_DIM is not supported by this build";
+    case FA_ERR_DTYPE: return "dtype must be fp16 or bf16";
+    case FA_ERR_STRIDE: return "the head-dim stride must be 1 and the other strides multiples of 8 elements";
+    case FA_ERR_ALIGN: return "tensor base pointers must be 16-byte aligned";
+    case FA_ERR_TILING: return "unsupported BLOCK_M/BLOCK_N combination";
+    case FA_ERR_SCALE: return "sm_scale must be finite";
+    case FA_ERR_GRID: return "the persistent program count must be >= 0";
+    case FA_ERR_LAUNCH: return "the HIP runtime rejected the kernel launch";
+    default: return "unknown fa_fwd status";
+  }
+}
+
+int fa_validate(const fa_fwd_params *p) {
+  if (p == nullptr) return FA_ERR_NULL;
+  if (p->B < 0 || p->H < 0 || p->Sq < 0 || p->Sk < 0 || p->D <= 0) return FA_ERR_SHAPE;
+  if (p->Sq > 0 && p->Sk == 0 && p->B > 0 && p->H > 0) return FA_ERR_SHAPE;
+  if (!is_supported_head_dim(p->D)) return FA_ERR_HEAD_DIM;
+  if (p->dtype != FA_DTYPE_FP16 && p->dtype != FA_DTYPE_BF16) return FA_ERR_DTYPE;
+  if (!(p->sm_scale == p->sm_scale) || isinf(p->sm_scale)) return FA_ERR_SCALE;
+  if (p->num_programs < 0) return FA_ERR_GRID;
+  if ((p->block_m == 0) != (p->block_n == 0)) return FA_ERR_TILING;
+  const bool empty = p->B == 0 || p->H == 0 || p->Sq == 0;
+  if (empty) return FA_OK;
+  if (p->q == nullptr || p->k == nullptr || p->v == nullptr || p->o == nullptr) return FA_ERR_NULL;
+  const int64_t *st[4] = {p->q_stride, p->k_stride, p->v_stride, p->o_stride};
+  const int64_t rows[4] = {p->Sq, p->Sk, p->Sk, p->Sq};
+  for (int t = 0; t < 4; ++t) {
+    if (st[t][3] != 1) return FA_ERR_STRIDE;
+    for (int i = 0; i < 3; ++i)
+      if (st[t][i] < 0 || st[t][i] % 8 != 0) return FA_ERR_STRIDE;
+    if (rows[t] > 1 && st[t][2] < p->D) return FA_ERR_STRIDE;
+    // Buffer offsets inside one (b, h) slice are 32-bit: keep the slice, plus
+    // the query rows of the last (partial) m-tile, below 2 GiB.
+    if ((rows[t] + kMaxBlockM) * (st[t][2] > p->D ? st[t][2] : p->D) * 2 >= ((int64_t)1 << 31))
+      return FA_ERR_SHAPE;
+  }
+  if ((int64_t)p->Sq * 4 >= ((int64_t)1 << 31)) return FA_ERR_SHAPE;
+  if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o)) return FA_ERR_ALIGN;
+  if (p->lse != nullptr && ((uintptr_t)p->lse & 3u) != 0) return FA_ERR_ALIGN;
+  Plan plan;
+  return make_plan(p, &plan);
+}
+
+int fa_query_config(const fa_fwd_params *p, int32_t out[FA_CFG_COUNT]) {
+  if (p == nullptr || out == nullptr) return FA_ERR_NULL;
+  if (p->B < 0 || p->H < 0 || p->Sq < 0 || p->Sk < 0) return FA_ERR_SHAPE;
+  if (!is_supported_head_dim(p->D)) return FA_ERR_HEAD_DIM;
+  if (p->dtype != FA_DTYPE_FP16 && p->dtype != FA_DTYPE_BF16) return FA_ERR_DTYPE;
+  if ((p->block_m == 0) != (p->block_n == 0)) return FA_ERR_TILING;
+  if (p->num_programs < 0) return FA_ERR_GRID;
+  Plan plan;
+  const int rc = make_plan(p, &plan);
+  if (rc != FA_OK) return rc;
+  out[FA_CFG_BLOCK_M] = plan.BM;
+  out[FA_CFG_BLOCK_N] = plan.BN;
+  out[FA_CFG_WAVES] = plan.NW;
+  out[FA_CFG_GRID] = plan.grid;
+  out[FA_CFG_TOTAL_TILES] = (int32_t)plan.total_tiles;
+  out[FA_CFG_LDS_BYTES] = kKernels[plan.kernel].lds_bytes;
+  out[FA_CFG_STAGE] = p->causal ? 3 : 1;
+  out[FA_CFG_KERNEL_ID] = plan.kernel;
+  return FA_OK;
+}
+
+int fa_num_kernels(void) { return kNumKernels; }
+
+int fa_params_size(void) { return (int)sizeof(fa_fwd_params); }
+
+int fa_kernel_info(int index, int32_t out[6]) {
+  if (out == nullptr) return FA_ERR_NULL;
+  if (index < 0 || index >= kNumKernels) return FA_ERR_TILING;
+  const KernelEntry &e = kKernels[index];
+  out[0] = e.D;
+  out[1] = e.dtype;
+  out[2] = e.causal;
+  out[3] = 32 * e.NW;
+  out[4] = e.BN;
+  out[5] = e.NW;
+  return FA_OK;
+}
+
+int fa_fwd(const fa_fwd_params *p, void *hip_stream) {
+  const int rc = fa_validate(p);
+  if (rc != FA_OK) return rc;
+  if (p->B == 0 || p->H == 0 || p->Sq == 0) return FA_OK;
+  Plan plan;
+  const int prc = make_plan(p, &plan);
+  if (prc != FA_OK) return prc;
+
+  KernelArgs a;
+  a.q = (const char *)p->q;
+  a.k = (const char *)p->k;
+  a.v = (const char *)p->v;
+  a.o = (char *)p->o;
+  a.lse = p->lse;
+  a.q_sb = p->q_stride[0]; a.q_sh = p->q_stride[1]; a.q_ss = p->q_stride[2];
+  a.k_sb = p->k_stride[0]; a.k_sh = p->k_stride[1]; a.k_ss = p->k_stride[2];
+  a.v_sb = p->v_stride[0]; a.v_sh = p->v_stride[1]; a.v_ss = p->v_stride[2];
+  a.o_sb = p->o_stride[0]; a.o_sh = p->o_stride[1]; a.o_ss = p->o_stride[2];
+  a.B = p->B;
+  a.H = p->H;
+  a.Sq = p->Sq;
+  a.Sk = p->Sk;
+  a.n_mtiles = plan.n_mtiles;
+  a.total_tiles = (int32_t)plan.total_tiles;
+  a.xcd_remap = plan.grid == plan.total_tiles ? 1 : 0;
+  // A negative scale is folded into Q (sign flip of every element, exact),
+  // a zero scale into a tiny positive one (all logits ~0: uniform weights).
+  const float s = p->sm_scale;
+  a.q_sign = s < 0.f ? 0x80008000u : 0u;
+  float c = fabsf(s) * kLog2e;
+  if (c < 1e-30f) c = 1e-30f;
+  a.c = c;
+
+  const KernelEntry &e = kKernels[plan.kernel];
+  hipStream_t stream = (hipStream_t)hip_stream;
+  hipLaunchKernelGGL(e.fn, dim3(plan.grid), dim3(64 * e.NW), 0, stream, a);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
+}
+
+}  // extern "C"

@@ -1,0 +1,345 @@
+"""FlashAttention forward for AMD Instinct MI355X -- drop-in for the reference
+module `flash_attention_forward.py` (ZyEng-Art/flash_attn_npu).
+
+Callers use this file exactly as they use the reference: import it, or load it
+by path (evaluate_attention.py:55-59 uses importlib's spec_from_file_location),
+read `DEVICE`, and call
+
+    attention(q, k, v, causal, sm_scale, BM=None, BN=None, return_lse=False)
+
+(flash_attention_forward.py:1197-1201).  `flash_attention_forward` is the same
+function under the name the task statement uses.  q, k, v are BNSD
+[Z, H, N_CTX, HEAD_DIM] fp16/bf16 tensors on the GPU; the result is O in the
+input dtype and, with return_lse=True, the fp32 natural-log row LSE [Z, H, N].
+
+Below this module is one C-ABI call (`fa_fwd` in libfa_mi355x.so, declared in
+include/fa_fwd.h) that launches the hand-written gfx950 kernel on the current
+stream.  There is no other implementation: without the library, or on a
+non-GPU tensor, the call raises.
+
+The file is self-contained (no package-relative imports) so it can be loaded
+by path like the reference.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from pathlib import Path
+
+import torch
+
+DEVICE = "cuda"
+RESULT_DIR_NAME = "result_dir"
+# 0 = one workgroup per (z, h, m-tile); >0 caps the grid and the kernel strides
+# over tiles (the reference's persistent grid, flash_attention_forward.py:24,616-623).
+DEFAULT_PERSISTENT_PROGRAMS = 0
+PROFILE_OP_NAME = "fa_fwd_kernel"
+LIB_NAME = "libfa_mi355x.so"
+SUPPORTED_HEAD_DIMS = (64, 128)
+# The reference accepts these head dims (flash_attention_forward.py:1121-1122).
+REFERENCE_HEAD_DIMS = (16, 32, 64, 128, 256)
+
+# BEGIN AUTO-TUNED DEFAULT TILING PRESETS
+# (Z, H, N_CTX, HEAD_DIM, causal) -> (BLOCK_M, BLOCK_N), rewritten by
+# tune_flash_attention_forward.py from gfx950 sweeps.
+DEFAULT_TILING_PRESETS = {
+}
+# END AUTO-TUNED DEFAULT TILING PRESETS
+
+# --------------------------------------------------------------------------
+# C ABI binding (include/fa_fwd.h)
+
+FA_OK = 0
+FA_ERR_LAUNCH = -100
+_ARGUMENT_ERRORS = {-1, -2, -3, -4, -5, -6, -7, -8, -9}
+FA_CFG_COUNT = 8
+FA_DTYPE = {torch.float16: 0, torch.bfloat16: 1}
+
+
+class FaFwdParams(ctypes.Structure):
+    """Mirror of `fa_fwd_params` (include/fa_fwd.h)."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("q_stride", ctypes.c_int64 * 4),
+        ("k_stride", ctypes.c_int64 * 4),
+        ("v_stride", ctypes.c_int64 * 4),
+        ("o_stride", ctypes.c_int64 * 4),
+        ("B", ctypes.c_int32),
+        ("H", ctypes.c_int32),
+        ("Sq", ctypes.c_int32),
+        ("Sk", ctypes.c_int32),
+        ("D", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("causal", ctypes.c_int32),
+        ("sm_scale", ctypes.c_float),
+        ("block_m", ctypes.c_int32),
+        ("block_n", ctypes.c_int32),
+        ("num_programs", ctypes.c_int32),
+    ]
+
+
+_LIB = None
+
+
+def library_path() -> Path:
+    override = os.environ.get("FA_MI355X_LIB")
+    if override:
+        return Path(override)
+    return Path(__file__).resolve().parent / LIB_NAME
+
+
+def _load_library():
+    """Load libfa_mi355x.so once; raise if it has not been built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = library_path()
+    if not path.exists():
+        raise RuntimeError(
+            f"{path} is missing: build it first (python -m flash_attn_npu_amd.build, "
+            "or __graft_entry__.build()). There is no fallback implementation."
+        )
+    lib = ctypes.CDLL(str(path))
+    P = ctypes.POINTER(FaFwdParams)
+    I32P = ctypes.POINTER(ctypes.c_int32)
+    lib.fa_fwd.argtypes = [P, ctypes.c_void_p]
+    lib.fa_fwd.restype = ctypes.c_int
+    lib.fa_validate.argtypes = [P]
+    lib.fa_validate.restype = ctypes.c_int
+    lib.fa_query_config.argtypes = [P, I32P]
+    lib.fa_query_config.restype = ctypes.c_int
+    lib.fa_error_string.argtypes = [ctypes.c_int]
+    lib.fa_error_string.restype = ctypes.c_char_p
+    lib.fa_abi_version.argtypes = []
+    lib.fa_abi_version.restype = ctypes.c_int
+    lib.fa_num_kernels.argtypes = []
+    lib.fa_num_kernels.restype = ctypes.c_int
+    lib.fa_kernel_info.argtypes = [ctypes.c_int, I32P]
+    lib.fa_kernel_info.restype = ctypes.c_int
+    lib.fa_params_size.argtypes = []
+    lib.fa_params_size.restype = ctypes.c_int
+    if lib.fa_params_size() != ctypes.sizeof(FaFwdParams):
+        raise RuntimeError("fa_fwd_params layout mismatch between the library and this binding")
+    _LIB = lib
+    return lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == FA_OK:
+        return
+    msg = f"{what}: {_load_library().fa_error_string(rc).decode()} (code {rc})"
+    if rc in _ARGUMENT_ERRORS:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def kernel_table():
+    """All kernel instances in the library: dicts of D, dtype, causal, BLOCK_M, BLOCK_N, waves."""
+    lib = _load_library()
+    out = (ctypes.c_int32 * 6)()
+    rows = []
+    for i in range(lib.fa_num_kernels()):
+        _check(lib.fa_kernel_info(i, out), "fa_kernel_info")
+        rows.append({"HEAD_DIM": out[0], "dtype": "bfloat16" if out[1] else "float16",
+                     "causal": bool(out[2]), "BLOCK_M": out[3], "BLOCK_N": out[4], "waves": out[5]})
+    return rows
+
+
+# --------------------------------------------------------------------------
+# Tiling policy (flash_attention_forward.py:156-252, 616-644)
+
+def _get_persistent_programs():
+    """Grid cap from $PERSISTENT_PROGRAMS (>= 1), else 0 = one workgroup per tile.
+
+    Same variable and check as flash_attention_forward.py:616-623.
+    """
+    raw = os.environ.get("PERSISTENT_PROGRAMS")
+    if raw is None:
+        return DEFAULT_PERSISTENT_PROGRAMS
+    value = int(raw)
+    if value < 1:
+        raise ValueError("PERSISTENT_PROGRAMS must be >= 1")
+    return value
+
+
+def _shape_params(z, h, n_ctx, head_dim, causal, bm=0, bn=0, dtype=torch.float16, programs=0):
+    p = FaFwdParams()
+    p.B, p.H, p.Sq, p.Sk, p.D = z, h, n_ctx, n_ctx, head_dim
+    p.dtype = FA_DTYPE.get(dtype, -1)
+    p.causal = 1 if causal else 0
+    p.sm_scale = 1.0
+    p.block_m, p.block_n = bm or 0, bn or 0
+    p.num_programs = programs
+    return p
+
+
+def _query_config(z, h, n_ctx, head_dim, causal, bm=0, bn=0, dtype=torch.float16, programs=0):
+    lib = _load_library()
+    out = (ctypes.c_int32 * FA_CFG_COUNT)()
+    p = _shape_params(z, h, n_ctx, head_dim, causal, bm, bn, dtype, programs)
+    _check(lib.fa_query_config(ctypes.byref(p), out), "fa_query_config")
+    return list(out)
+
+
+def _default_tiling(z, h, n_ctx, head_dim, causal):
+    """Preset for this exact shape, else the library's gfx950 default."""
+    preset = DEFAULT_TILING_PRESETS.get((z, h, n_ctx, head_dim, causal))
+    if preset is not None:
+        return preset
+    cfg = _query_config(z, h, n_ctx, head_dim, causal)
+    return cfg[0], cfg[1]
+
+
+def get_tiling(z, h, n_ctx, head_dim, causal):
+    return _default_tiling(z, h, n_ctx, head_dim, causal)
+
+
+def get_tiling_source(z, h, n_ctx, head_dim, causal):
+    if (z, h, n_ctx, head_dim, causal) in DEFAULT_TILING_PRESETS:
+        return "preset"
+    return "fallback"
+
+
+def _resolve_tiling(z, h, n_ctx, head_dim, causal, bm=None, bn=None):
+    if (bm is None) != (bn is None):
+        raise ValueError("BM and BN must be provided together")
+    if bm is not None:
+        return bm, bn, "override"
+    return (*get_tiling(z, h, n_ctx, head_dim, causal), get_tiling_source(z, h, n_ctx, head_dim, causal))
+
+
+def _describe_runtime(z, h, n_ctx, head_dim, causal, bm=None, bn=None):
+    block_m, block_n, tiling_source = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn)
+    cfg = _query_config(z, h, n_ctx, head_dim, causal, block_m, block_n,
+                        programs=_get_persistent_programs())
+    return {
+        "selected_config": {"BLOCK_M": cfg[0], "BLOCK_N": cfg[1]},
+        "tiling_source": tiling_source,
+        "total_tiles": cfg[4],
+        "launched_programs": cfg[3],
+        "stage": cfg[6],
+        "waves": cfg[2],
+        "lds_bytes": cfg[5],
+        "kernel_id": cfg[7],
+    }
+
+
+# --------------------------------------------------------------------------
+# Operator
+
+def _validate_inputs(q, k, v):
+    """The reference's checks (flash_attention_forward.py:1114-1122) plus dtype/device."""
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, v must all be 4D tensors shaped [Z, H, N_CTX, HEAD_DIM]")
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k, v must have the same shape")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("q, k, v must be on the same device")
+    if q.shape[-1] not in REFERENCE_HEAD_DIMS:
+        raise ValueError("HEAD_DIM must be one of {16, 32, 64, 128, 256}")
+    if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"HEAD_DIM={q.shape[-1]} is not supported by this build "
+                         f"(supported: {SUPPORTED_HEAD_DIMS})")
+    if q.dtype not in FA_DTYPE or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k, v must all be float16 or all be bfloat16")
+    if q.device.type != "cuda":
+        raise ValueError(f"q, k, v must be GPU tensors (device 'cuda'), got {q.device}")
+
+
+def _kernel_ready(t):
+    """A view the kernel can read directly: dim stride 1, other strides %8, 16B-aligned."""
+    st = t.stride()
+    if st[3] != 1 or any(s % 8 for s in st[:3]) or t.data_ptr() % 16:
+        return t.contiguous()
+    if t.shape[2] > 1 and st[2] < t.shape[3]:
+        return t.contiguous()
+    return t
+
+
+def _fill_strides(arr, t):
+    for i, s in enumerate(t.stride()):
+        arr[i] = s
+
+
+def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
+    """Validate, resolve tiling, allocate O/LSE, launch; returns (out, lse).
+
+    Same flow and return value as flash_attention_forward.py:1130-1194.
+    """
+    _validate_inputs(q, k, v)
+    z, h, n_ctx, head_dim = q.shape
+    bm, bn, _ = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn)
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    out = torch.empty_like(q)
+    lse = torch.empty((z, h, n_ctx), device=q.device, dtype=torch.float32)
+    if out.numel() == 0:
+        return out, lse
+    out = _kernel_ready(out)
+    sm_scale = float(sm_scale)
+    if not math.isfinite(sm_scale):
+        raise ValueError("sm_scale must be finite")
+
+    lib = _load_library()
+    p = FaFwdParams()
+    p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
+    _fill_strides(p.q_stride, q)
+    _fill_strides(p.k_stride, k)
+    _fill_strides(p.v_stride, v)
+    _fill_strides(p.o_stride, out)
+    p.B, p.H, p.Sq, p.Sk, p.D = z, h, n_ctx, n_ctx, head_dim
+    p.dtype = FA_DTYPE[q.dtype]
+    p.causal = 1 if causal else 0
+    p.sm_scale = sm_scale
+    p.block_m, p.block_n = int(bm), int(bn)
+    p.num_programs = _get_persistent_programs()
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        _check(lib.fa_fwd(ctypes.byref(p), ctypes.c_void_p(stream)), "fa_fwd")
+    return out, lse
+
+
+def attention(q, k, v, causal, sm_scale, BM=None, BN=None, return_lse=False):
+    out, lse = _launch_kernel(q, k, v, causal, sm_scale, bm=BM, bn=BN)
+    if return_lse:
+        return out, lse
+    return out
+
+
+flash_attention_forward = attention
+
+
+def _dtype_from_name(name):
+    normalized = name.strip().lower()
+    if normalized in {"float16", "fp16"}:
+        return torch.float16
+    if normalized in {"bfloat16", "bf16"}:
+        return torch.bfloat16
+    raise ValueError(f"Unsupported dtype: {name}")
+
+
+def _make_inputs(z, h, n_ctx, head_dim, dtype):
+    """N(0, 0.5) q, k, v on DEVICE, as flash_attention_forward.py:1308-1312."""
+    q = torch.empty((z, h, n_ctx, head_dim), dtype=dtype, device=DEVICE).normal_(mean=0.0, std=0.5)
+    k = torch.empty((z, h, n_ctx, head_dim), dtype=dtype, device=DEVICE).normal_(mean=0.0, std=0.5)
+    v = torch.empty((z, h, n_ctx, head_dim), dtype=dtype, device=DEVICE).normal_(mean=0.0, std=0.5)
+    return q, k, v
+
+
+__all__ = [
+    "DEVICE",
+    "RESULT_DIR_NAME",
+    "PROFILE_OP_NAME",
+    "DEFAULT_TILING_PRESETS",
+    "get_tiling",
+    "get_tiling_source",
+    "attention",
+    "flash_attention_forward",
+    "kernel_table",
+]

@@ -1,0 +1,174 @@
+"""CPU oracle for the FlashAttention forward path.
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this module, and only as the checker (or the timed
+CPU baseline).  The product path (flash_attn_npu_amd) never calls it: on a
+machine without the HIP library the product raises instead of falling back.
+
+What it restates
+----------------
+`attention_ref` is the reference's fp32 formula `_torch_attention_reference`
+(evaluate_attention.py:134-143), written against numpy instead of torch:
+
+    scores = (q.float() @ k.float()^T) * sm_scale            (:135)
+    causal: scores[i, j] = -inf for j > i  (triu(ones, diagonal=1))   (:136-141)
+    probs  = softmax(scores, dim=-1) in fp32                 (:142)
+    out    = (probs @ v.float()).to(q.dtype)                 (:143)
+
+and adds the natural-log row LSE that the reference kernel stores next to O
+(`m_i += log(l_i)`, flash_attention_forward.py:1022, stored fp32 [Z,H,N] at
+:1031, allocated at :1136): lse[i] = log(sum_j exp(scores[i, j])) over the
+visible keys, i.e. over the *scaled* logits.  The causal convention is the
+reference's mask `offs_m >= curr_n` (flash_attention_forward.py:694-696):
+key j is visible to query i iff j <= i.
+
+`attention_bruteforce` recomputes the same quantities one row at a time in
+float64 with math.exp (a different algorithm: explicit loops, no BLAS); it is
+used on tiny inputs to pin `attention_ref`.
+
+Rounding helpers produce the fp16 / bf16 values the GPU path writes, so that
+an output can be compared to the oracle after the same final cast the
+reference applies (`.to(q.dtype)`, evaluate_attention.py:143).
+
+Pinning status: attention_ref and the LSE are pinned by the brute-force loops,
+closed forms (zero logits, first causal row, one-hot selection), shift
+invariance, the causal-prefix identity and scipy's logsumexp/softmax
+(tests/test_oracle.py).  The reference itself cannot execute here (it needs
+torch_npu and an Ascend NPU), so there is no reference-produced tensor to
+compare against; its only numeric artefact, the accuracy envelope in
+evaluation_reports/evaluation_report.txt:10-36, is not a tensor.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+__all__ = [
+    "attention_ref",
+    "attention_bruteforce",
+    "round_bf16",
+    "round_fp16",
+    "round_to",
+    "attention_flops",
+]
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> nearest bfloat16 (round to nearest even), returned as float32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    out = rounded.astype(np.uint32).view(np.float32)
+    # NaN must stay NaN (the add above could carry a NaN payload into Inf).
+    return np.where(np.isnan(x), np.float32(np.nan), out)
+
+
+def round_fp16(x: np.ndarray) -> np.ndarray:
+    """float32 -> nearest IEEE half (round to nearest even), returned as float32."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def round_to(x: np.ndarray, dtype: str | None) -> np.ndarray:
+    """Apply the final `.to(q.dtype)` of evaluate_attention.py:143."""
+    if dtype is None or dtype in ("float32", "fp32"):
+        return np.asarray(x, dtype=np.float32)
+    if dtype in ("bfloat16", "bf16"):
+        return round_bf16(x)
+    if dtype in ("float16", "fp16"):
+        return round_fp16(x)
+    raise ValueError(f"unsupported dtype {dtype!r}")
+
+
+def _causal_mask(sq: int, sk: int) -> np.ndarray:
+    # True where the key is masked: triu(ones(sq, sk), diagonal=1), as in
+    # evaluate_attention.py:137-140.
+    return np.triu(np.ones((sq, sk), dtype=bool), k=1)
+
+
+def attention_ref(q, k, v, causal: bool, sm_scale: float, out_dtype: str | None = None,
+                  compute_dtype=np.float32):
+    """fp32 softmax(sm_scale * q k^T [+ causal mask]) v and the natural-log LSE.
+
+    q: [..., Sq, D], k, v: [..., Sk, D] (any leading batch/head dims), holding
+    the exact values of the fp16/bf16 inputs as float32.  Returns
+    (out, lse): out [..., Sq, D] rounded to `out_dtype` (float32 values),
+    lse [..., Sq] float32.  Heads are processed one at a time, so memory stays
+    O(Sq * Sk) per head.
+    """
+    q = np.asarray(q, dtype=np.float32)
+    k = np.asarray(k, dtype=np.float32)
+    v = np.asarray(v, dtype=np.float32)
+    if q.ndim < 2 or k.shape[:-2] != q.shape[:-2] or v.shape[:-1] != k.shape[:-1]:
+        raise ValueError("q, k, v must share leading dims; k and v must share Sk")
+    if q.shape[-1] != k.shape[-1]:
+        raise ValueError("q and k must share the head dim")
+    lead = q.shape[:-2]
+    sq, d = q.shape[-2:]
+    sk = k.shape[-2]
+    dv = v.shape[-1]
+    qf = q.reshape(-1, sq, d)
+    kf = k.reshape(-1, sk, d)
+    vf = v.reshape(-1, sk, dv)
+    out = np.empty((qf.shape[0], sq, dv), dtype=np.float32)
+    lse = np.empty((qf.shape[0], sq), dtype=np.float32)
+    mask = _causal_mask(sq, sk) if causal else None
+    ct = compute_dtype
+    for i in range(qf.shape[0]):
+        scores = (qf[i].astype(ct) @ kf[i].astype(ct).T) * ct(sm_scale)
+        if mask is not None:
+            scores = np.where(mask, ct(-np.inf), scores)
+        row_max = scores.max(axis=-1, keepdims=True)
+        # Rows with no visible key (only possible when Sq > Sk is not the
+        # case for top-left causal) would give -inf max; keep them finite.
+        safe_max = np.where(np.isfinite(row_max), row_max, ct(0))
+        e = np.exp(scores - safe_max)
+        denom = e.sum(axis=-1, keepdims=True)
+        probs = e / denom
+        out[i] = (probs @ vf[i].astype(ct)).astype(np.float32)
+        lse[i] = (np.log(denom[..., 0]) + safe_max[..., 0]).astype(np.float32)
+    out = out.reshape(*lead, sq, dv)
+    lse = lse.reshape(*lead, sq)
+    return round_to(out, out_dtype), lse
+
+
+def attention_bruteforce(q, k, v, causal: bool, sm_scale: float):
+    """Row-by-row float64 restatement with explicit loops (tiny inputs only).
+
+    For each query row i: logits s_j = sm_scale * sum_d q[i,d] k[j,d] over the
+    visible keys j (j <= i when causal), m = max_j s_j,
+    lse = m + log(sum_j exp(s_j - m)), out[i, :] = sum_j exp(s_j - lse) v[j, :].
+    q, k, v: [Sq, D], [Sk, D], [Sk, Dv].  Returns float64 (out, lse).
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    sq, d = q.shape
+    sk = k.shape[0]
+    out = np.zeros((sq, v.shape[1]), dtype=np.float64)
+    lse = np.zeros(sq, dtype=np.float64)
+    for i in range(sq):
+        last = min(i, sk - 1) if causal else sk - 1
+        logits = []
+        for j in range(last + 1):
+            acc = 0.0
+            for t in range(d):
+                acc += q[i, t] * k[j, t]
+            logits.append(sm_scale * acc)
+        m = max(logits)
+        total = 0.0
+        for s in logits:
+            total += math.exp(s - m)
+        lse[i] = m + math.log(total)
+        for j, s in enumerate(logits):
+            w = math.exp(s - lse[i])
+            for t in range(v.shape[1]):
+                out[i, t] += w * v[j, t]
+    return out, lse
+
+
+def attention_flops(b: int, h: int, sq: int, sk: int, d: int, causal: bool) -> float:
+    """Algorithmic FLOPs of one forward: 4*B*H*Sq*Sk*D, halved when causal."""
+    f = 4.0 * b * h * sq * sk * d
+    return f / 2.0 if causal else f
