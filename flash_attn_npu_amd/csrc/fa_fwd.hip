@@ -417,27 +417,363 @@ fa_fwd_kernel(KernelArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Kernel v2: K and V tiles reach LDS by direct DMA (buffer_load ... lds), stay
+// row-major there, and are read as MFMA operands with ds_read_b128 (K) and
+// the gfx950 transpose read ds_read_b64_tr_b16 (V^T), so no VGPR or VALU is
+// spent moving or transposing tiles.  NSTAGE LDS stages form a ring; tile
+// t + NSTAGE - 1 is in flight while tile t is computed.
+//
+// LDS row r (one key, 2*D bytes) stores its 16-byte chunks XOR-swizzled by
+// swz(r) = ((r & 3) << 1) | ((r >> 2) & 1).  With that, the 8 lanes of a
+// ds_read_b128 phase (8 consecutive keys, one chunk) and the 16 lanes of a
+// ds_read_b64_tr_b16 phase (4 consecutive keys, two chunks) each touch
+// distinct banks, while every DMA instruction still writes 1 KB contiguously
+// and reads whole rows from HBM.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) char lds_char;
+
+__device__ __forceinline__ u32x2_t lds_read_tr16(const char *smem_base, uint32_t off) {
+  const lds_char *p = (const lds_char *)smem_base + off;
+  i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t *)p);
+  return __builtin_bit_cast(u32x2_t, v);
+}
+
+// One 16-byte-per-lane DMA: lane i writes LDS bytes [lds + 16 i, +16) with
+// the buffer bytes at voff (out-of-range reads give zeros).  Issued as inline
+// asm so the compiler does not treat later LDS reads as aliasing the
+// in-flight DMA (it would insert vmcnt(0) before them and serialise the
+// prefetch); completion is enforced explicitly with s_waitcnt vmcnt + barrier
+// before a stage is read.  M0 carries the LDS base and is set right here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(BufRsrc r, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// sched_group_barrier masks.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+
+template <int D, int BN, int NW, int NSTAGE>
+struct Cfg2 {
+  static constexpr int BM = 32 * NW;
+  static constexpr int NT = 64 * NW;
+  static constexpr int ROW = 2 * D;           // bytes per K/V row in LDS
+  static constexpr int CPR = ROW / 16;        // 16-byte chunks per row
+  static constexpr int RPI = 1024 / ROW;      // rows per DMA instruction (64 lanes x 16 B)
+  static constexpr int TILE = BN * ROW;       // bytes of one K (or V) tile
+  static constexpr int IPT = TILE / 1024;     // DMA instructions per tile and tensor
+  static constexpr int IPW = IPT / NW;        // ... per wave
+  static constexpr int STAGE = 2 * TILE;
+  static constexpr int LDS_BYTES = NSTAGE * STAGE;
+  static_assert(CPR >= 8, "the swizzle needs at least 8 chunks per row");
+  static_assert(IPT % NW == 0 && IPW >= 1, "DMA instructions must split evenly over waves");
+  static_assert(BN % 32 == 0 && D % 32 == 0, "tile shape");
+  static_assert(NSTAGE >= 2 && NSTAGE <= 4, "stages");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one gfx950 CU");
+};
+
+template <int D, int BN, int NW, int NSTAGE, bool BF16, bool CAUSAL>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+fa_fwd_dma_kernel(KernelArgs p) {
+  using C = Cfg2<D, BN, NW, NSTAGE>;
+  constexpr int BM = C::BM;
+  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31;
+  const int h = lane >> 5;
+
+  // DMA: instruction j of this wave fills LDS rows (wave + j*NW)*RPI .. +RPI of
+  // the tile; lane -> (row, physical chunk), and it fetches the logical chunk
+  // that the swizzle stores there.
+  uint32_t dk[C::IPW], dv[C::IPW];
+#pragma unroll
+  for (int j = 0; j < C::IPW; ++j) {
+    const int row = (wave + j * NW) * C::RPI + lane / C::CPR;
+    const int lc = (lane % C::CPR) ^ swz(row);
+    dk[j] = (uint32_t)(row * p.k_ss * 2 + lc * 16);
+    dv[j] = (uint32_t)(row * p.v_ss * 2 + lc * 16);
+  }
+  // K operand reads: lane (h, n) reads key row 32kb + n, logical chunk 2s + h.
+  uint32_t kro[4];
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) kro[s4] = (uint32_t)(n * C::ROW + (((2 * s4 + h) ^ swz(n)) * 16));
+  // V^T operand reads (transpose): in lane group g = lane/16, source lane
+  // 4j + c points at key row 16ks + 8e + 4h + j, dims 32db + 16(g&1) + 4c.
+  uint32_t vro[2];
+  {
+    const int g = lane >> 4, sg = lane & 15, jj = sg >> 2, cc = sg & 3;
+#pragma unroll
+    for (int par = 0; par < 2; ++par)
+      vro[par] = (uint32_t)((4 * h + jj) * C::ROW +
+                            (((4 * par + 2 * (g & 1) + (cc >> 1)) ^ ((jj << 1) | h)) * 16) + (cc & 1) * 8);
+  }
+
+  const float c = p.c;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_char *)smem;
+
+  for (int slot = blockIdx.x; slot < p.total_tiles; slot += gridDim.x) {
+    const int L = logical_tile(slot, gridDim.x, p.xcd_remap);
+    const int bh = L / p.n_mtiles;
+    const int mr = L - bh * p.n_mtiles;
+    const int mt = CAUSAL ? (p.n_mtiles - 1 - mr) : mr;
+    const int bb = bh / p.H;
+    const int hh = bh - bb * p.H;
+
+    const int q0 = mt * BM;
+    const int q0w = q0 + 32 * wave;
+    const int qrow = q0w + n;
+
+    const char *qg = p.q + 2 * (bb * p.q_sb + hh * p.q_sh);
+    const char *kg = p.k + 2 * (bb * p.k_sb + hh * p.k_sh);
+    const char *vg = p.v + 2 * (bb * p.v_sb + hh * p.v_sh);
+
+    const int kv_end = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
+    const int n_tiles = (kv_end + BN - 1) / BN;
+    const int wave_last_q = q0w + 31;
+
+    auto issue_tile = [&](int t) {
+      const int key0 = t * BN;
+      const uint32_t nbk = (uint32_t)((int64_t)(p.Sk - key0) * p.k_ss * 2);
+      const uint32_t nbv = (uint32_t)((int64_t)(p.Sk - key0) * p.v_ss * 2);
+      const BufRsrc rk = make_rsrc(kg + (int64_t)key0 * p.k_ss * 2, nbk);
+      const BufRsrc rv = make_rsrc(vg + (int64_t)key0 * p.v_ss * 2, nbv);
+      const uint32_t st = lds_base + (uint32_t)((t % NSTAGE) * C::STAGE);
+#pragma unroll
+      for (int j = 0; j < C::IPW; ++j) {
+        const uint32_t lo = st + (uint32_t)((wave + j * NW) * 1024);
+        dma16(rk, lo, dk[j]);
+        dma16(rv, lo + C::TILE, dv[j]);
+      }
+    };
+
+    // Prologue: the first NSTAGE-1 tiles in flight.
+#pragma unroll
+    for (int t = 0; t < NSTAGE - 1; ++t)
+      if (t < n_tiles) issue_tile(t);
+
+    u32x4_t qf[D / 16];
+    {
+      const BufRsrc rq = make_rsrc(qg, (uint32_t)((int64_t)p.Sq * p.q_ss * 2));
+      const uint32_t qo = (uint32_t)(qrow * p.q_ss * 2 + 16 * h);
+#pragma unroll
+      for (int s = 0; s < D / 16; ++s) qf[s] = buf_load16(rq, qo + 32 * s) ^ p.q_sign;
+    }
+
+    f32x16_t oacc[D / 32];
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) oacc[db] = (f32x16_t){};
+    float m_run = -INFINITY;
+    float l_run = 0.f;
+
+    for (int t = 0; t < n_tiles; ++t) {
+      // Wait for this wave's DMA of tile t (later tiles may stay in flight),
+      // then for every wave's (barrier).  The barrier also retires all reads
+      // of the stage that the next issue overwrites.
+      if (NSTAGE >= 3 && t + 1 < n_tiles) {
+        __builtin_amdgcn_s_waitcnt(0x0f70 | ((2 * C::IPW) & 0xf) | (((2 * C::IPW) >> 4) << 14));
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+      }
+      __syncthreads();
+      if (t + NSTAGE - 1 < n_tiles) issue_tile(t + NSTAGE - 1);
+
+      const int kbase = t * BN;
+      if (CAUSAL && kbase > wave_last_q) continue;
+
+      const uint32_t st = (uint32_t)((t % NSTAGE) * C::STAGE);
+      uint32_t ka[4];
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) ka[s4] = st + kro[s4];
+      const uint32_t va0 = st + C::TILE + vro[0];
+      const uint32_t va1 = st + C::TILE + vro[1];
+
+      // S^T = K Q^T.  Fragment i = (s, kb); K fragments are read KPF ahead of
+      // their MFMA, and the first VPF V^T fragments of the P*V product are
+      // issued right behind them so they land during the softmax.
+      constexpr int NQK = (D / 16) * (BN / 32);
+      constexpr int KPF = 4;
+      constexpr int NPV = (BN / 16) * (D / 32);
+      constexpr int VPF = 2;
+      auto vread = [&](int i) {
+        const int ks = i / (D / 32), db = i % (D / 32);
+        const uint32_t base = (db & 1) ? va1 : va0;
+        const uint32_t imm = (uint32_t)(16 * ks * C::ROW + 128 * (db >> 1));
+        const u32x2_t lo = lds_read_tr16(smem, base + imm);
+        const u32x2_t hi = lds_read_tr16(smem, base + imm + 8 * C::ROW);
+        return (u32x4_t){lo[0], lo[1], hi[0], hi[1]};
+      };
+      u32x4_t kfr[NQK];
+      u32x4_t vfr[NPV];
+      f32x16_t sacc[BN / 32];
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb) sacc[kb] = (f32x16_t){};
+#pragma unroll
+      for (int i = 0; i < NQK; ++i) {
+        const int s = i / (BN / 32), kb = i % (BN / 32);
+        kfr[i] = *(const u32x4_t *)(smem + ka[s & 3] + (32 * kb * C::ROW + 128 * (s >> 2)));
+      }
+#pragma unroll
+      for (int i = 0; i < VPF; ++i) vfr[i] = vread(i);
+#pragma unroll
+      for (int i = 0; i < NQK; ++i) {
+        const int s = i / (BN / 32), kb = i % (BN / 32);
+        sacc[kb] = mfma32x32x16<BF16>(kfr[i], qf[s], sacc[kb]);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, KPF, 0);
+#pragma unroll
+      for (int i = 0; i < NQK - KPF; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * VPF, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, KPF, 0);
+
+      const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && kbase + BN - 1 > q0w);
+      if (need_mask) {
+        const int last_key = CAUSAL ? min(qrow, p.Sk - 1) : p.Sk - 1;
+        const int lim = last_key - kbase - 4 * h;
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int off = 32 * kb + 8 * (r >> 2) + (r & 3);
+            sacc[kb][r] = off <= lim ? sacc[kb][r] : -INFINITY;
+          }
+      }
+
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+      mx = halves_max(mx);
+      const float m_cand = mx * c;
+      const bool upd = m_cand > m_run + kLazyMaxThreshold;
+      const float m_new = upd ? m_cand : m_run;
+      if (__builtin_amdgcn_ballot_w64(upd)) {
+        const float alpha = upd ? fast_exp2(m_run - m_new) : 1.f;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) oacc[db] *= alpha;
+      }
+      m_run = m_new;
+      const float mb = (m_new == -INFINITY) ? 0.f : m_new;
+
+      float lsum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = fast_exp2(__builtin_fmaf(sacc[kb][r], c, -mb));
+          sacc[kb][r] = pv;
+          lsum[r & 3] += pv;
+        }
+      l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+
+      u32x4_t pf[BN / 16];
+#pragma unroll
+      for (int ks = 0; ks < BN / 16; ++ks) {
+        const int kb = ks >> 1, t8 = (ks & 1) * 8;
+        pf[ks][0] = pack2<BF16>(sacc[kb][t8 + 0], sacc[kb][t8 + 1]);
+        pf[ks][1] = pack2<BF16>(sacc[kb][t8 + 2], sacc[kb][t8 + 3]);
+        pf[ks][2] = pack2<BF16>(sacc[kb][t8 + 4], sacc[kb][t8 + 5]);
+        pf[ks][3] = pack2<BF16>(sacc[kb][t8 + 6], sacc[kb][t8 + 7]);
+      }
+
+      // O^T += V^T P^T; the A operand is two transpose reads (keys +0..3 and
+      // +8..11 of the k-step), VPF fragments ahead of their MFMA.
+#pragma unroll
+      for (int i = VPF; i < NPV; ++i) vfr[i] = vread(i);
+#pragma unroll
+      for (int i = 0; i < NPV; ++i) {
+        const int ks = i / (D / 32), db = i % (D / 32);
+        oacc[db] = mfma32x32x16<BF16>(vfr[i], pf[ks], oacc[db]);
+      }
+#pragma unroll
+      for (int i = 0; i < NPV - VPF; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, VPF, 0);
+    }
+
+    const float l_tot = halves_sum(l_run);
+    const float inv = 1.f / l_tot;
+    {
+      const char *og = p.o + 2 * (bb * p.o_sb + hh * p.o_sh);
+      const BufRsrc ro = make_rsrc(og, (uint32_t)((int64_t)p.Sq * p.o_ss * 2));
+      const uint32_t oo = (uint32_t)(qrow * p.o_ss * 2 + 8 * h);
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          u32x2_t x;
+          x[0] = pack2<BF16>(oacc[db][4 * j + 0] * inv, oacc[db][4 * j + 1] * inv);
+          x[1] = pack2<BF16>(oacc[db][4 * j + 2] * inv, oacc[db][4 * j + 3] * inv);
+          buf_store8(x, ro, oo + 2 * (32 * db + 8 * j));
+        }
+    }
+    if (p.lse != nullptr) {
+      const uint32_t nbytes = (uint32_t)p.Sq * 4u;
+      const BufRsrc rl = make_rsrc(p.lse + ((int64_t)bb * p.H + hh) * p.Sq, nbytes);
+      const float lse = (m_run + __log2f(l_tot)) * kLn2;
+      buf_store4(__builtin_bit_cast(uint32_t, lse), rl, h ? nbytes : (uint32_t)qrow * 4u);
+    }
+    if (slot + (int)gridDim.x < p.total_tiles) __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Kernel table.
 typedef void (*KernelFn)(KernelArgs);
 
 struct KernelEntry {
   int32_t D, dtype, causal, BN, NW;
+  int32_t stages;  // LDS stages of the DMA kernel; 0 = register-staged kernel
   int32_t lds_bytes;
   KernelFn fn;
 };
 
 template <int D, int BN, int NW, bool BF16, bool CAUSAL>
 constexpr KernelEntry entry() {
-  return KernelEntry{D, BF16 ? 1 : 0, CAUSAL ? 1 : 0, BN, NW,
+  return KernelEntry{D, BF16 ? 1 : 0, CAUSAL ? 1 : 0, BN, NW, 0,
                      FaConfig<D, BN, NW, BF16, CAUSAL>::LDS_BYTES,
                      fa_fwd_kernel<D, BN, NW, BF16, CAUSAL>};
+}
+
+template <int D, int BN, int NW, int NSTAGE, bool BF16, bool CAUSAL>
+constexpr KernelEntry entry_dma() {
+  return KernelEntry{D, BF16 ? 1 : 0, CAUSAL ? 1 : 0, BN, NW, NSTAGE,
+                     Cfg2<D, BN, NW, NSTAGE>::LDS_BYTES,
+                     fa_fwd_dma_kernel<D, BN, NW, NSTAGE, BF16, CAUSAL>};
 }
 
 #define FA_ENTRIES_DT_C(D, BN, NW)                                                   \
   entry<D, BN, NW, false, false>(), entry<D, BN, NW, false, true>(),                 \
       entry<D, BN, NW, true, false>(), entry<D, BN, NW, true, true>()
+#define FA_DMA_ENTRIES(D, BN, NW, ST)                                                \
+  entry_dma<D, BN, NW, ST, false, false>(), entry_dma<D, BN, NW, ST, false, true>(), \
+      entry_dma<D, BN, NW, ST, true, false>(), entry_dma<D, BN, NW, ST, true, true>()
 
 const KernelEntry kKernels[] = {
+#ifdef FA_PREFER_REGISTER_STAGED
+    FA_ENTRIES_DT_C(64, 64, 4),
+    FA_ENTRIES_DT_C(128, 64, 4),
+#endif
+    FA_DMA_ENTRIES(128, 64, 4, 2),
+    FA_DMA_ENTRIES(128, 64, 8, 3),
+    FA_DMA_ENTRIES(64, 64, 4, 2),
+    FA_DMA_ENTRIES(64, 64, 8, 3),
     FA_ENTRIES_DT_C(64, 64, 4),
     FA_ENTRIES_DT_C(128, 64, 4),
 };
