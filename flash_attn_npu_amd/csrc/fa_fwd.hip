@@ -39,6 +39,8 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "fa_fwd.h"
 
 namespace {
@@ -59,6 +61,21 @@ constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLazyMaxThreshold = 8.0f;
 constexpr int kNumXcd = 8;
 constexpr int kMaxBlockM = 256;  // largest BLOCK_M of any kernel instance
+constexpr int kRowMargin = 1024; // rows addressed past a tensor's end (>= BLOCK_M, >= NR * BLOCK_N)
+#ifndef FA_FP16_DOT_SUM
+#define FA_FP16_DOT_SUM 1
+#endif
+constexpr bool kFp16DotSum = FA_FP16_DOT_SUM != 0;
+#ifndef FA_MFMA_PRIO
+#define FA_MFMA_PRIO 0
+#endif
+// FA_TIMING (development builds only): the ping-pong kernel accumulates, per
+// wave, the shader-clock cycles spent in each phase and writes them to
+// KernelArgs::timing.  The product build compiles none of it.
+#ifdef FA_TIMING
+#define FA_CLK() ((uint32_t)__builtin_amdgcn_s_memtime())
+#define FA_CLK_DELTA(a, b) ((b) - (a))
+#endif
 
 struct KernelArgs {
   const char *q;
@@ -74,8 +91,10 @@ struct KernelArgs {
   int32_t n_mtiles;     // ceil(Sq / BM)
   int32_t total_tiles;  // n_mtiles * B * H
   int32_t xcd_remap;    // 1: grid == total_tiles, keep logical neighbours on one XCD
+  int32_t head_group;   // heads whose m-tiles are scheduled together (causal order)
   uint32_t q_sign;      // 0x80008000 when sm_scale < 0 (Q is negated in registers)
   float c;              // |sm_scale| * log2(e), > 0
+  uint32_t *timing;     // per-wave phase cycle counts (FA_TIMING builds only), else null
 };
 
 template <bool BF16>
@@ -163,6 +182,28 @@ __device__ __forceinline__ int logical_tile(int bid, int grid, int remap) {
   return prefix + bid / kNumXcd;
 }
 
+// Logical tile -> (head index bh, m-tile).  Heads are taken in groups of
+// `group` (sized so that one group's m-tiles fill one XCD's workgroup slots):
+// the m-tiles of a group run together and share K/V through the XCD's L2.
+// Causal: inside a group, tiles go heaviest (largest m) first across the
+// group's heads, so the last workgroups dispatched are the cheapest ones.
+__device__ __forceinline__ void decode_tile(int L, int n_mtiles, int BH, int group, bool causal,
+                                            int *bh, int *mt) {
+  if (!causal || group <= 1) {
+    *bh = L / n_mtiles;
+    const int mr = L - *bh * n_mtiles;
+    *mt = causal ? (n_mtiles - 1 - mr) : mr;
+    return;
+  }
+  const int span = group * n_mtiles;
+  const int gi = L / span;
+  const int r = L - gi * span;
+  const int gsz = min(group, BH - gi * group);
+  const int mr = r / gsz;
+  *bh = gi * group + (r - mr * gsz);
+  *mt = n_mtiles - 1 - mr;
+}
+
 template <int D, int BN, int NW, bool BF16, bool CAUSAL>
 struct FaConfig {
   static constexpr int BM = 32 * NW;           // query rows per workgroup
@@ -220,9 +261,8 @@ fa_fwd_kernel(KernelArgs p) {
 
   for (int slot = blockIdx.x; slot < p.total_tiles; slot += gridDim.x) {
     const int L = logical_tile(slot, gridDim.x, p.xcd_remap);
-    const int bh = L / p.n_mtiles;
-    const int mr = L - bh * p.n_mtiles;
-    const int mt = CAUSAL ? (p.n_mtiles - 1 - mr) : mr;  // causal: heaviest first
+    int bh, mt;
+    decode_tile(L, p.n_mtiles, p.B * p.H, p.head_group, CAUSAL, &bh, &mt);  // causal: heaviest first
     const int bb = bh / p.H;
     const int hh = bh - bb * p.H;
 
@@ -424,12 +464,26 @@ fa_fwd_kernel(KernelArgs p) {
 // t + NSTAGE - 1 is in flight while tile t is computed.
 //
 // LDS row r (one key, 2*D bytes) stores its 16-byte chunks XOR-swizzled by
-// swz(r) = ((r & 3) << 1) | ((r >> 2) & 1).  With that, the 8 lanes of a
-// ds_read_b128 phase (8 consecutive keys, one chunk) and the 16 lanes of a
-// ds_read_b64_tr_b16 phase (4 consecutive keys, two chunks) each touch
-// distinct banks, while every DMA instruction still writes 1 KB contiguously
-// and reads whole rows from HBM.
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// swz<D>(r).  The LDS has 64 banks of 4 bytes (256 bytes per bank row):
+//  * D = 128 (256-byte rows, 16 chunks): swz = 4 (r & 3) + ((r >> 2) & 3), a
+//    permutation over any 16 consecutive rows, so the 16 lanes of a
+//    ds_read_b128 phase (16 consecutive keys, one logical chunk) hit 16
+//    distinct bank slots; and for the 4 consecutive rows of a transpose read
+//    the high two bits (r & 3) separate their 4-chunk blocks.
+//  * D = 64 (128-byte rows, two per bank row): swz = 4 ((r >> 1) & 1) +
+//    ((r >> 2) & 3), a permutation over r >> 1 within each half of the bank
+//    row, with rows r and r + 2 of a transpose read in different 4-chunk
+//    blocks.
+// Every DMA instruction still writes 1 KB contiguously and reads whole rows
+// from HBM.
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (D == 128) {
+    return ((r & 3) << 2) | ((r >> 2) & 3);
+  } else {
+    return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  }
+}
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) char lds_char;
@@ -499,23 +553,30 @@ fa_fwd_dma_kernel(KernelArgs p) {
 #pragma unroll
   for (int j = 0; j < C::IPW; ++j) {
     const int row = (wave + j * NW) * C::RPI + lane / C::CPR;
-    const int lc = (lane % C::CPR) ^ swz(row);
+    const int lc = (lane % C::CPR) ^ swz<D>(row);
     dk[j] = (uint32_t)(row * p.k_ss * 2 + lc * 16);
     dv[j] = (uint32_t)(row * p.v_ss * 2 + lc * 16);
   }
-  // K operand reads: lane (h, n) reads key row 32kb + n, logical chunk 2s + h.
-  uint32_t kro[4];
+  // K operand reads: lane (h, n) reads key row 32kb + n, logical chunk 2s + h
+  // (swz(32kb + n) == swz(n)).
+  uint32_t kro[D / 16];
 #pragma unroll
-  for (int s4 = 0; s4 < 4; ++s4) kro[s4] = (uint32_t)(n * C::ROW + (((2 * s4 + h) ^ swz(n)) * 16));
+  for (int s = 0; s < D / 16; ++s) kro[s] = (uint32_t)(n * C::ROW + (((2 * s + h) ^ swz<D>(n)) * 16));
   // V^T operand reads (transpose): in lane group g = lane/16, source lane
-  // 4j + c points at key row 16ks + 8e + 4h + j, dims 32db + 16(g&1) + 4c.
-  uint32_t vro[2];
+  // 4j + c points at key row 16ks + 8e + 4h + j, dims 32db + 16(g&1) + 4c
+  // (logical chunk 4db + 2(g&1) + c/2).  swz of that row depends only on
+  // (e, h, j), so one lane offset per (db, e) covers every k-step ks.
+  uint32_t vro[D / 32][2];
   {
     const int g = lane >> 4, sg = lane & 15, jj = sg >> 2, cc = sg & 3;
 #pragma unroll
-    for (int par = 0; par < 2; ++par)
-      vro[par] = (uint32_t)((4 * h + jj) * C::ROW +
-                            (((4 * par + 2 * (g & 1) + (cc >> 1)) ^ ((jj << 1) | h)) * 16) + (cc & 1) * 8);
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int row = 8 * e + 4 * h + jj;
+        const int lc = 4 * db + 2 * (g & 1) + (cc >> 1);
+        vro[db][e] = (uint32_t)((4 * h + jj) * C::ROW + ((lc ^ swz<D>(row)) * 16) + (cc & 1) * 8);
+      }
   }
 
   const float c = p.c;
@@ -523,9 +584,8 @@ fa_fwd_dma_kernel(KernelArgs p) {
 
   for (int slot = blockIdx.x; slot < p.total_tiles; slot += gridDim.x) {
     const int L = logical_tile(slot, gridDim.x, p.xcd_remap);
-    const int bh = L / p.n_mtiles;
-    const int mr = L - bh * p.n_mtiles;
-    const int mt = CAUSAL ? (p.n_mtiles - 1 - mr) : mr;
+    int bh, mt;
+    decode_tile(L, p.n_mtiles, p.B * p.H, p.head_group, CAUSAL, &bh, &mt);
     const int bb = bh / p.H;
     const int hh = bh - bb * p.H;
 
@@ -575,10 +635,13 @@ fa_fwd_dma_kernel(KernelArgs p) {
     float m_run = -INFINITY;
     float l_run = 0.f;
 
-    for (int t = 0; t < n_tiles; ++t) {
-      // Wait for this wave's DMA of tile t (later tiles may stay in flight),
-      // then for every wave's (barrier).  The barrier also retires all reads
-      // of the stage that the next issue overwrites.
+    // One KV tile: wait for its DMA, barrier, refill the ring, then
+    // S^T = K Q^T, online softmax, O^T += V^T P^T.  MASKED is a compile-time
+    // switch: only tiles crossing the diagonal or the ragged key tail pay for
+    // the mask (and for skipping tiles above a wave's own rows), and neither
+    // loop body branches on it.
+    auto kv_tile = [&](int t, auto masked_tag) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
       if (NSTAGE >= 3 && t + 1 < n_tiles) {
         __builtin_amdgcn_s_waitcnt(0x0f70 | ((2 * C::IPW) & 0xf) | (((2 * C::IPW) >> 4) << 14));
       } else {
@@ -588,14 +651,9 @@ fa_fwd_dma_kernel(KernelArgs p) {
       if (t + NSTAGE - 1 < n_tiles) issue_tile(t + NSTAGE - 1);
 
       const int kbase = t * BN;
-      if (CAUSAL && kbase > wave_last_q) continue;
+      if (MASKED && CAUSAL && kbase > wave_last_q) return;
 
       const uint32_t st = (uint32_t)((t % NSTAGE) * C::STAGE);
-      uint32_t ka[4];
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) ka[s4] = st + kro[s4];
-      const uint32_t va0 = st + C::TILE + vro[0];
-      const uint32_t va1 = st + C::TILE + vro[1];
 
       // S^T = K Q^T.  Fragment i = (s, kb); K fragments are read KPF ahead of
       // their MFMA, and the first VPF V^T fragments of the P*V product are
@@ -606,12 +664,12 @@ fa_fwd_dma_kernel(KernelArgs p) {
       constexpr int VPF = 2;
       auto vread = [&](int i) {
         const int ks = i / (D / 32), db = i % (D / 32);
-        const uint32_t base = (db & 1) ? va1 : va0;
-        const uint32_t imm = (uint32_t)(16 * ks * C::ROW + 128 * (db >> 1));
-        const u32x2_t lo = lds_read_tr16(smem, base + imm);
-        const u32x2_t hi = lds_read_tr16(smem, base + imm + 8 * C::ROW);
+        const uint32_t imm = st + (uint32_t)(C::TILE + 16 * ks * C::ROW);
+        const u32x2_t lo = lds_read_tr16(smem, vro[db][0] + imm);
+        const u32x2_t hi = lds_read_tr16(smem, vro[db][1] + imm + 8 * C::ROW);
         return (u32x4_t){lo[0], lo[1], hi[0], hi[1]};
       };
+      if (FA_MFMA_PRIO) __builtin_amdgcn_s_setprio(FA_MFMA_PRIO);
       u32x4_t kfr[NQK];
       u32x4_t vfr[NPV];
       f32x16_t sacc[BN / 32];
@@ -620,7 +678,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
 #pragma unroll
       for (int i = 0; i < NQK; ++i) {
         const int s = i / (BN / 32), kb = i % (BN / 32);
-        kfr[i] = *(const u32x4_t *)(smem + ka[s & 3] + (32 * kb * C::ROW + 128 * (s >> 2)));
+        kfr[i] = *(const u32x4_t *)(smem + st + kro[s] + 32 * kb * C::ROW);
       }
 #pragma unroll
       for (int i = 0; i < VPF; ++i) vfr[i] = vread(i);
@@ -638,8 +696,10 @@ fa_fwd_dma_kernel(KernelArgs p) {
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * VPF, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, KPF, 0);
 
-      const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && kbase + BN - 1 > q0w);
-      if (need_mask) {
+      if (FA_MFMA_PRIO) __builtin_amdgcn_s_setprio(0);
+      if (MASKED) {
+        // Register r of block kb holds key kbase + 4h + (32kb + 8(r>>2) + (r&3));
+        // it is visible iff that offset <= lim.
         const int last_key = CAUSAL ? min(qrow, p.Sk - 1) : p.Sk - 1;
         const int lim = last_key - kbase - 4 * h;
 #pragma unroll
@@ -676,22 +736,38 @@ fa_fwd_dma_kernel(KernelArgs p) {
         for (int r = 0; r < 16; ++r) {
           const float pv = fast_exp2(__builtin_fmaf(sacc[kb][r], c, -mb));
           sacc[kb][r] = pv;
-          lsum[r & 3] += pv;
+          if (BF16 || !kFp16DotSum) lsum[r & 3] += pv;
         }
-      l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
 
+      // P^T fragments: k-step ks (16 keys) = registers 8t..8t+7 of block ks/2.
+      // fp16 P is also summed here, two rounded values per v_dot2_f32_f16
+      // (fp16 keeps 11 bits, far inside the LSE tolerance; bf16 keeps 8 and
+      // is summed in fp32 above instead).  The dot takes the f16x2 produced
+      // by the conversion itself: taking it back out of the packed dword with
+      // a bit_cast of a vector element is miscompiled by this toolchain (only
+      // element 0 survives).
       u32x4_t pf[BN / 16];
+      const f16x2_t ones_h = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
       for (int ks = 0; ks < BN / 16; ++ks) {
         const int kb = ks >> 1, t8 = (ks & 1) * 8;
-        pf[ks][0] = pack2<BF16>(sacc[kb][t8 + 0], sacc[kb][t8 + 1]);
-        pf[ks][1] = pack2<BF16>(sacc[kb][t8 + 2], sacc[kb][t8 + 3]);
-        pf[ks][2] = pack2<BF16>(sacc[kb][t8 + 4], sacc[kb][t8 + 5]);
-        pf[ks][3] = pack2<BF16>(sacc[kb][t8 + 6], sacc[kb][t8 + 7]);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const f32x2_t pair = {sacc[kb][t8 + 2 * w], sacc[kb][t8 + 2 * w + 1]};
+          if constexpr (BF16) {
+            pf[ks][w] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pair, bf16x2_t));
+          } else {
+            const f16x2_t hv = __builtin_convertvector(pair, f16x2_t);
+            pf[ks][w] = __builtin_bit_cast(uint32_t, hv);
+            if (kFp16DotSum) lsum[w] = __builtin_amdgcn_fdot2(hv, ones_h, lsum[w], false);
+          }
+        }
       }
+      l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
 
       // O^T += V^T P^T; the A operand is two transpose reads (keys +0..3 and
       // +8..11 of the k-step), VPF fragments ahead of their MFMA.
+      if (FA_MFMA_PRIO) __builtin_amdgcn_s_setprio(FA_MFMA_PRIO);
 #pragma unroll
       for (int i = VPF; i < NPV; ++i) vfr[i] = vread(i);
 #pragma unroll
@@ -705,7 +781,16 @@ fa_fwd_dma_kernel(KernelArgs p) {
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
       }
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, VPF, 0);
-    }
+      if (FA_MFMA_PRIO) __builtin_amdgcn_s_setprio(0);
+    };
+
+    // Tiles visible to every query of the workgroup need no mask.
+    int n_full = p.Sk / BN;
+    if (CAUSAL) n_full = min(n_full, (q0 + 1) / BN);
+    n_full = min(n_full, n_tiles);
+    int t = 0;
+    for (; t < n_full; ++t) kv_tile(t, std::integral_constant<bool, false>{});
+    for (; t < n_tiles; ++t) kv_tile(t, std::integral_constant<bool, true>{});
 
     const float l_tot = halves_sum(l_run);
     const float inv = 1.f / l_tot;
@@ -730,6 +815,423 @@ fa_fwd_dma_kernel(KernelArgs p) {
       buf_store4(__builtin_bit_cast(uint32_t, lse), rl, h ? nbytes : (uint32_t)qrow * 4u);
     }
     if (slot + (int)gridDim.x < p.total_tiles) __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel v3 ("ping-pong"): 8 waves in two groups of 4.  Waves w and w + 4
+// share a SIMD.  Every wave runs the same action list
+//     M(0) S(0) M(1) S(1) ... M(n)
+// with  M(t) = O^T += V^T(t-1) P^T(t-1) and S^T(t) = K(t) Q^T  (32 MFMAs) and
+//       S(t) = online softmax of S^T(t) -> P(t), rescale O  (VALU),
+// one action per barrier interval, group 1 one interval behind group 0: in
+// every interval one wave of each SIMD issues MFMAs while the other runs the
+// softmax, so the matrix core is fed while the exp/max/sum work proceeds.
+// K and V tiles come in by DMA into two LDS rings of NR slots each.  K(t) is
+// read in intervals 2t, 2t+1 and V(t) in 2t+2, 2t+3; at the start of
+// interval 2j the DMAs for K(j + NR - 1) and V(j + NR - 2) are issued into
+// the slots freed by K(j - 1) and V(j - 2), so every tile has 2 NR - 2
+// intervals to arrive.  Past the last tile the same DMAs are issued against an
+// empty buffer range (they write zeros into free slots), which keeps the
+// number in flight, and so the vmcnt allowance, uniform.
+template <int D, int BN, int NR>
+struct Cfg3 {
+  static constexpr int NW = 8;
+  static constexpr int BM = 32 * NW;
+  static constexpr int ROW = 2 * D;
+  static constexpr int CPR = ROW / 16;
+  static constexpr int RPI = 1024 / ROW;
+  static constexpr int TILE = BN * ROW;
+  static constexpr int IPT = TILE / 1024;
+  static constexpr int IPW = IPT / NW;
+  static constexpr int K_OFF = 0;
+  static constexpr int V_OFF = NR * TILE;
+  static constexpr int LDS_BYTES = 2 * NR * TILE;
+  static_assert(CPR >= 8 && IPT % NW == 0 && IPW >= 1, "tile shape");
+  static_assert(NR >= 3 && NR <= 6, "ring depth");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one gfx950 CU");
+};
+
+// s_waitcnt immediate: vmcnt(n), no wait on expcnt / lgkmcnt.
+constexpr int vmcnt_imm(int n) { return 0x0f70 | (n & 0xf) | ((n >> 4) << 14); }
+
+template <int D, int BN, int NR, bool BF16, bool CAUSAL>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+fa_fwd_pp_kernel(KernelArgs p) {
+  using C = Cfg3<D, BN, NR>;
+  constexpr int NW = C::NW;
+  constexpr int BM = C::BM;
+  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;
+  // 32-row blocks alternate between the groups, so diagonal tiles cost both
+  // groups about the same.
+  const int rblk = 2 * (wave & 3) + grp;
+  const int n = lane & 31;
+  const int h = lane >> 5;
+
+  uint32_t dk[C::IPW], dv[C::IPW];
+#pragma unroll
+  for (int j = 0; j < C::IPW; ++j) {
+    const int row = (wave + j * NW) * C::RPI + lane / C::CPR;
+    const int lc = (lane % C::CPR) ^ swz<D>(row);
+    dk[j] = (uint32_t)(row * p.k_ss * 2 + lc * 16);
+    dv[j] = (uint32_t)(row * p.v_ss * 2 + lc * 16);
+  }
+  uint32_t kro[D / 16];
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s) kro[s] = (uint32_t)(n * C::ROW + (((2 * s + h) ^ swz<D>(n)) * 16));
+  uint32_t vro[D / 32][2];
+  {
+    const int g = lane >> 4, sg = lane & 15, jj = sg >> 2, cc = sg & 3;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int row = 8 * e + 4 * h + jj;
+        const int lc = 4 * db + 2 * (g & 1) + (cc >> 1);
+        vro[db][e] = (uint32_t)((4 * h + jj) * C::ROW + ((lc ^ swz<D>(row)) * 16) + (cc & 1) * 8);
+      }
+  }
+
+  const float c = p.c;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_char *)smem;
+
+  for (int slot = blockIdx.x; slot < p.total_tiles; slot += gridDim.x) {
+#ifdef FA_TIMING
+    uint32_t tm_m = 0, tm_s = 0, tm_w = 0, tm_dma = 0, tm_pro = 0, tm_epi = 0, n_m = 0, n_s = 0;
+    const uint32_t tm0 = FA_CLK();
+    uint32_t tmark = tm0;
+#endif
+    const int L = logical_tile(slot, gridDim.x, p.xcd_remap);
+    int bh, mt;
+    decode_tile(L, p.n_mtiles, p.B * p.H, p.head_group, CAUSAL, &bh, &mt);
+    const int bb = bh / p.H;
+    const int hh = bh - bb * p.H;
+
+    const int q0 = mt * BM;
+    const int q0w = q0 + 32 * rblk;
+    const int qrow = q0w + n;
+
+    const char *qg = p.q + 2 * (bb * p.q_sb + hh * p.q_sh);
+    const char *kg = p.k + 2 * (bb * p.k_sb + hh * p.k_sh);
+    const char *vg = p.v + 2 * (bb * p.v_sb + hh * p.v_sh);
+
+    const int kv_end = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
+    const int n_tiles = (kv_end + BN - 1) / BN;
+    const int wave_last_q = q0w + 31;
+    // Tiles [0, n_full) are visible to every row of this wave (no mask);
+    // tile t is active for this wave iff some key of it is visible.
+    int n_full = p.Sk / BN;
+    if (CAUSAL) n_full = min(n_full, (q0w + 1) / BN);
+    n_full = min(n_full, n_tiles);
+    auto active = [&](int t) { return !CAUSAL || t * BN <= wave_last_q; };
+
+    // DMA of K(t) / V(t) into ring slot t % NR.  One descriptor per (b, h)
+    // spans keys [0, Sk); the tile offset rides in the lane offset, so rows
+    // at or past Sk (ragged tail, tiles past the end) read as zeros.
+    const BufRsrc rk = make_rsrc(kg, (uint32_t)((int64_t)p.Sk * p.k_ss * 2));
+    const BufRsrc rv = make_rsrc(vg, (uint32_t)((int64_t)p.Sk * p.v_ss * 2));
+    const uint32_t k_tile_bytes = (uint32_t)(BN * p.k_ss * 2);
+    const uint32_t v_tile_bytes = (uint32_t)(BN * p.v_ss * 2);
+    auto issue_k = [&](int t) {
+      const uint32_t st = lds_base + (uint32_t)(C::K_OFF + (t % NR) * C::TILE);
+      const uint32_t off = (uint32_t)t * k_tile_bytes;
+#pragma unroll
+      for (int j = 0; j < C::IPW; ++j) dma16(rk, st + (uint32_t)((wave + j * NW) * 1024), dk[j] + off);
+    };
+    auto issue_v = [&](int t) {
+      const uint32_t st = lds_base + (uint32_t)(C::V_OFF + (t % NR) * C::TILE);
+      const uint32_t off = (uint32_t)t * v_tile_bytes;
+#pragma unroll
+      for (int j = 0; j < C::IPW; ++j) dma16(rv, st + (uint32_t)((wave + j * NW) * 1024), dv[j] + off);
+    };
+
+    u32x4_t qf[D / 16];
+    {
+      const BufRsrc rq = make_rsrc(qg, (uint32_t)((int64_t)p.Sq * p.q_ss * 2));
+      const uint32_t qo = (uint32_t)(qrow * p.q_ss * 2 + 16 * h);
+#pragma unroll
+      for (int s = 0; s < D / 16; ++s) qf[s] = buf_load16(rq, qo + 32 * s) ^ p.q_sign;
+    }
+    // Prologue: K(0 .. NR-2) and V(0 .. NR-3); Q and these have landed
+    // (this wave's), then everyone's.
+    issue_k(0);
+#pragma unroll
+    for (int i = -(NR - 2); i < 0; ++i) {
+      issue_k(i + NR - 1);
+      if (i + NR - 2 >= 0) issue_v(i + NR - 2);
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+#ifdef FA_TIMING
+    { const uint32_t now = FA_CLK(); tm_pro += FA_CLK_DELTA(tmark, now); tmark = now; }
+#endif
+
+    f32x16_t oacc[D / 32];
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) oacc[db] = (f32x16_t){};
+    float m_run = -INFINITY;
+    float l_run = 0.f;
+    f32x16_t sacc[BN / 32];
+    u32x4_t pf[BN / 16];
+
+    // Interval k starts (after the previous barrier) by issuing, when k = 2j,
+    // the DMAs for K(j + NR - 1) and V(j + NR - 2), and ends with a barrier.
+    // Before the barrier that opens interval 2j this wave's DMAs of K(j) and
+    // V(j - 1) have landed: only the groups issued in the last min(NR - 2, j)
+    // even intervals may still be in flight.
+    int k = 0;
+#ifdef FA_TIMING
+    uint32_t tphase = 0;
+#define FA_TAG_M() (tm_m += tphase, ++n_m)
+#define FA_TAG_S() (tm_s += tphase, ++n_s)
+#else
+#define FA_TAG_M() ((void)0)
+#define FA_TAG_S() ((void)0)
+#endif
+    auto interval_start = [&]() {
+#ifdef FA_TIMING
+      tmark = FA_CLK();
+#endif
+      if ((k & 1) == 0) {
+        const int j = k >> 1;
+        issue_k(j + NR - 1);
+        issue_v(j + NR - 2);
+      }
+    };
+    auto interval_end = [&]() {
+#ifdef FA_TIMING
+      const uint32_t tend = FA_CLK();
+#endif
+      if (k & 1) {
+        const int j = (k + 1) >> 1;
+        constexpr int G = 2 * C::IPW;  // DMA instructions per group
+        if (j >= NR - 2) {
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm((NR - 2) * G));
+        } else if (j == 1) {
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm(G));
+        } else if (j == 2) {
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * G));
+        } else {
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * G));
+        }
+      }
+#ifdef FA_TIMING
+      const uint32_t tdma = FA_CLK();
+      tm_dma += FA_CLK_DELTA(tend, tdma);
+#endif
+      __syncthreads();
+      ++k;
+#ifdef FA_TIMING
+      tm_w += FA_CLK_DELTA(tdma, FA_CLK());
+      tphase = FA_CLK_DELTA(tmark, tend);
+#endif
+    };
+
+    // M(t): PV(t-1) then QK(t), operand reads MPF MFMAs ahead.
+    auto mphase = [&](int t, auto pv_tag, auto qk_tag) {
+      constexpr bool DO_PV = decltype(pv_tag)::value;
+      constexpr bool DO_QK = decltype(qk_tag)::value;
+      constexpr int NPV = DO_PV ? (BN / 16) * (D / 32) : 0;
+      constexpr int NQK = DO_QK ? (D / 16) * (BN / 32) : 0;
+      constexpr int NOPS = NPV + NQK;
+      constexpr int MPF = 3;
+      const uint32_t stv = (uint32_t)(C::V_OFF + ((t + NR - 1) % NR) * C::TILE);
+      const uint32_t stk = (uint32_t)(C::K_OFF + (t % NR) * C::TILE);
+      u32x4_t fr[NOPS > 0 ? NOPS : 1];
+#pragma unroll
+      for (int i = 0; i < NOPS; ++i) {
+        if (i < NPV) {
+          const int ks = i / (D / 32), db = i % (D / 32);
+          const uint32_t imm = stv + (uint32_t)(16 * ks * C::ROW);
+          const u32x2_t lo = lds_read_tr16(smem, vro[db][0] + imm);
+          const u32x2_t hi = lds_read_tr16(smem, vro[db][1] + imm + 8 * C::ROW);
+          fr[i] = (u32x4_t){lo[0], lo[1], hi[0], hi[1]};
+        } else {
+          const int j = i - NPV;
+          const int s = j / (BN / 32), kb = j % (BN / 32);
+          fr[i] = *(const u32x4_t *)(smem + stk + kro[s] + 32 * kb * C::ROW);
+        }
+      }
+      if constexpr (DO_QK) {
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb) sacc[kb] = (f32x16_t){};
+      }
+#pragma unroll
+      for (int i = 0; i < NOPS; ++i) {
+        if (i < NPV) {
+          const int ks = i / (D / 32), db = i % (D / 32);
+          oacc[db] = mfma32x32x16<BF16>(fr[i], pf[ks], oacc[db]);
+        } else {
+          const int j = i - NPV;
+          const int s = j / (BN / 32), kb = j % (BN / 32);
+          sacc[kb] = mfma32x32x16<BF16>(fr[i], qf[s], sacc[kb]);
+        }
+      }
+      // Pin the order: reads of the first MPF ops, then one MFMA and the
+      // reads of the op MPF ahead, and so on.
+#pragma unroll
+      for (int i = 0; i < (MPF < NOPS ? MPF : NOPS); ++i) {
+        if (i < NPV) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        else __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+#pragma unroll
+      for (int i = 0; i + MPF < NOPS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        if (i + MPF < NPV) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        else __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, MPF < NOPS ? MPF : NOPS, 0);
+    };
+
+    // S(t): mask (diagonal / ragged tail only), online softmax, rescale O, P(t).
+    auto sphase = [&](int t, auto masked_tag) {
+      constexpr bool MASKED = decltype(masked_tag)::value;
+      const int kbase = t * BN;
+      if (MASKED) {
+        const int last_key = CAUSAL ? min(qrow, p.Sk - 1) : p.Sk - 1;
+        const int lim = last_key - kbase - 4 * h;
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int off = 32 * kb + 8 * (r >> 2) + (r & 3);
+            sacc[kb][r] = off <= lim ? sacc[kb][r] : -INFINITY;
+          }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+      mx = halves_max(mx);
+      const float m_cand = mx * c;
+      const bool upd = m_cand > m_run + kLazyMaxThreshold;
+      const float m_new = upd ? m_cand : m_run;
+      if (__builtin_amdgcn_ballot_w64(upd)) {
+        const float alpha = upd ? fast_exp2(m_run - m_new) : 1.f;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) oacc[db] *= alpha;
+      }
+      m_run = m_new;
+      const float mb = (m_new == -INFINITY) ? 0.f : m_new;
+      float lsum[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = fast_exp2(__builtin_fmaf(sacc[kb][r], c, -mb));
+          sacc[kb][r] = pv;
+          lsum[r & 3] += pv;
+        }
+      l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+#pragma unroll
+      for (int ks = 0; ks < BN / 16; ++ks) {
+        const int kb = ks >> 1, t8 = (ks & 1) * 8;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) pf[ks][w] = pack2<BF16>(sacc[kb][t8 + 2 * w], sacc[kb][t8 + 2 * w + 1]);
+      }
+    };
+
+    // Action list of this wave: M(0) S(0) ... M(n_act-1) S(n_act-1) M(n_act),
+    // M(n_act) being P*V only, then idle intervals up to 2 n_tiles + 1
+    // actions (tiles beyond n_act are above this wave's rows).  Visibility is
+    // monotone in t, so the loops below need no per-tile branching.
+    using T_ = std::integral_constant<bool, true>;
+    using F_ = std::integral_constant<bool, false>;
+    int n_act = n_tiles;
+    if (CAUSAL) n_act = min(n_act, wave_last_q / BN + 1);
+    if (grp == 1) {  // group 1 starts one interval late
+      interval_start();
+      interval_end();
+    }
+    // t = 0 (n_act >= 1 always): QK only.
+    interval_start();
+    mphase(0, F_{}, T_{});
+    interval_end();
+    FA_TAG_M();
+    interval_start();
+    if (0 < n_full) sphase(0, F_{}); else sphase(0, T_{});
+    interval_end();
+    FA_TAG_S();
+    int t = 1;
+    for (; t < n_full; ++t) {
+      interval_start();
+      mphase(t, T_{}, T_{});
+      interval_end();
+      FA_TAG_M();
+      interval_start();
+      sphase(t, F_{});
+      interval_end();
+      FA_TAG_S();
+    }
+    for (; t < n_act; ++t) {
+      interval_start();
+      mphase(t, T_{}, T_{});
+      interval_end();
+      FA_TAG_M();
+      interval_start();
+      sphase(t, T_{});
+      interval_end();
+      FA_TAG_S();
+    }
+    interval_start();
+    mphase(n_act, T_{}, F_{});
+    interval_end();
+    FA_TAG_M();
+    for (int idle = 2 * (n_tiles - n_act); idle > 0; --idle) {
+      interval_start();
+      interval_end();
+    }
+    if (grp == 0) {  // group 0's last interval is idle
+      interval_start();
+      interval_end();
+    }
+
+    const float l_tot = halves_sum(l_run);
+    const float inv = 1.f / l_tot;
+    {
+      const char *og = p.o + 2 * (bb * p.o_sb + hh * p.o_sh);
+      const BufRsrc ro = make_rsrc(og, (uint32_t)((int64_t)p.Sq * p.o_ss * 2));
+      const uint32_t oo = (uint32_t)(qrow * p.o_ss * 2 + 8 * h);
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          u32x2_t x;
+          x[0] = pack2<BF16>(oacc[db][4 * j + 0] * inv, oacc[db][4 * j + 1] * inv);
+          x[1] = pack2<BF16>(oacc[db][4 * j + 2] * inv, oacc[db][4 * j + 3] * inv);
+          buf_store8(x, ro, oo + 2 * (32 * db + 8 * j));
+        }
+    }
+    if (p.lse != nullptr) {
+      const uint32_t nbytes = (uint32_t)p.Sq * 4u;
+      const BufRsrc rl = make_rsrc(p.lse + ((int64_t)bb * p.H + hh) * p.Sq, nbytes);
+      const float lse = (m_run + __log2f(l_tot)) * kLn2;
+      buf_store4(__builtin_bit_cast(uint32_t, lse), rl, h ? nbytes : (uint32_t)qrow * 4u);
+    }
+#ifdef FA_TIMING
+#undef FA_TAG_M
+#undef FA_TAG_S
+    if (p.timing != nullptr && lane == 0) {
+      const uint32_t now = FA_CLK();
+      tm_epi = FA_CLK_DELTA(tmark, now);
+      uint32_t *dst = p.timing + ((int64_t)L * 8 + wave) * 8;
+      dst[0] = tm_m; dst[1] = tm_s; dst[2] = tm_w; dst[3] = tm_pro; dst[4] = tm_dma;
+      dst[5] = FA_CLK_DELTA(tm0, now); dst[6] = n_m; dst[7] = n_s;
+    }
+#endif
+    // The DMAs issued past the last tile may still be writing zeros into the
+    // rings: retire them (every wave) before a next tile reuses the slots.
+    if (slot + (int)gridDim.x < p.total_tiles) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+      __syncthreads();
+    }
   }
 }
 
@@ -761,6 +1263,11 @@ constexpr KernelEntry entry_dma() {
 #define FA_ENTRIES_DT_C(D, BN, NW)                                                   \
   entry<D, BN, NW, false, false>(), entry<D, BN, NW, false, true>(),                 \
       entry<D, BN, NW, true, false>(), entry<D, BN, NW, true, true>()
+#define FA_PP_ENTRIES(D, BN, NR)                                                     \
+  KernelEntry{D, 0, 0, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, fa_fwd_pp_kernel<D, BN, NR, false, false>}, \
+  KernelEntry{D, 0, 1, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, fa_fwd_pp_kernel<D, BN, NR, false, true>},  \
+  KernelEntry{D, 1, 0, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, fa_fwd_pp_kernel<D, BN, NR, true, false>},  \
+  KernelEntry{D, 1, 1, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, fa_fwd_pp_kernel<D, BN, NR, true, true>}
 #define FA_DMA_ENTRIES(D, BN, NW, ST)                                                \
   entry_dma<D, BN, NW, ST, false, false>(), entry_dma<D, BN, NW, ST, false, true>(), \
       entry_dma<D, BN, NW, ST, true, false>(), entry_dma<D, BN, NW, ST, true, true>()
@@ -771,9 +1278,9 @@ const KernelEntry kKernels[] = {
     FA_ENTRIES_DT_C(128, 64, 4),
 #endif
     FA_DMA_ENTRIES(128, 64, 4, 2),
-    FA_DMA_ENTRIES(128, 64, 8, 3),
+    FA_PP_ENTRIES(128, 64, 4),
     FA_DMA_ENTRIES(64, 64, 4, 2),
-    FA_DMA_ENTRIES(64, 64, 8, 3),
+    FA_PP_ENTRIES(64, 64, 4),
     FA_ENTRIES_DT_C(64, 64, 4),
     FA_ENTRIES_DT_C(128, 64, 4),
 };
@@ -834,6 +1341,13 @@ bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 }  // namespace
 
+#ifdef FA_TIMING
+static uint32_t *g_timing_buffer = nullptr;
+extern "C" void fa_set_timing_buffer(void *p) { g_timing_buffer = (uint32_t *)p; }
+#else
+static uint32_t *const g_timing_buffer = nullptr;
+#endif
+
 extern "C" {
 
 int fa_abi_version(void) { return FA_ABI_VERSION; }
@@ -875,8 +1389,9 @@ int fa_validate(const fa_fwd_params *p) {
       if (st[t][i] < 0 || st[t][i] % 8 != 0) return FA_ERR_STRIDE;
     if (rows[t] > 1 && st[t][2] < p->D) return FA_ERR_STRIDE;
     // Buffer offsets inside one (b, h) slice are 32-bit: keep the slice, plus
-    // the query rows of the last (partial) m-tile, below 2 GiB.
-    if ((rows[t] + kMaxBlockM) * (st[t][2] > p->D ? st[t][2] : p->D) * 2 >= ((int64_t)1 << 31))
+    // the rows past its end that a last partial m-tile or the DMAs issued past
+    // the last KV tile address, below 2 GiB.
+    if ((rows[t] + kRowMargin) * (st[t][2] > p->D ? st[t][2] : p->D) * 2 >= ((int64_t)1 << 31))
       return FA_ERR_SHAPE;
   }
   if ((int64_t)p->Sq * 4 >= ((int64_t)1 << 31)) return FA_ERR_SHAPE;
@@ -948,7 +1463,21 @@ int fa_fwd(const fa_fwd_params *p, void *hip_stream) {
   a.Sk = p->Sk;
   a.n_mtiles = plan.n_mtiles;
   a.total_tiles = (int32_t)plan.total_tiles;
+#ifdef FA_NO_XCD_REMAP
+  a.xcd_remap = 0;
+#else
   a.xcd_remap = plan.grid == plan.total_tiles ? 1 : 0;
+#endif
+  // One XCD has 32 CUs; a 256-row (8-wave) workgroup fills a CU, a 128-row
+  // one half of it.  Group enough heads that their m-tiles fill the XCD.
+  {
+    const int slots = (plan.NW == 8 ? 32 : 64);
+#ifdef FA_HEAD_GROUP
+    a.head_group = FA_HEAD_GROUP;
+#else
+    a.head_group = plan.n_mtiles >= slots ? 1 : (slots + plan.n_mtiles - 1) / plan.n_mtiles;
+#endif
+  }
   // A negative scale is folded into Q (sign flip of every element, exact),
   // a zero scale into a tiny positive one (all logits ~0: uniform weights).
   const float s = p->sm_scale;
@@ -956,6 +1485,7 @@ int fa_fwd(const fa_fwd_params *p, void *hip_stream) {
   float c = fabsf(s) * kLog2e;
   if (c < 1e-30f) c = 1e-30f;
   a.c = c;
+  a.timing = g_timing_buffer;
 
   const KernelEntry &e = kKernels[plan.kernel];
   hipStream_t stream = (hipStream_t)hip_stream;
