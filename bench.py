@@ -38,32 +38,46 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def read_traffic(workload_tag: str):
-    """HBM bytes per launch measured with rocprofv3 --pmc, if a summary exists.
+def profile_summary_path(workload_tag: str) -> Path:
+    return REPO / "profiles" / f"fa_fwd_{workload_tag}_rocprof.txt"
 
-    profiles/<tag>_traffic.txt holds lines `fetch_bytes=<int>` and
-    `write_bytes=<int>` (per dispatch, already scaled by the copy-kernel
-    calibration factor recorded in the same file).
+
+def read_traffic(workload_tag: str):
+    """HBM bytes per launch from the committed rocprofv3 summary, if present.
+
+    The summary (written by flash_attn_npu_amd.rocprof from FETCH_SIZE and
+    WRITE_SIZE passes, each scaled by what the same counter reads for a plain
+    256 MiB device copy in the same process) carries hbm_read_bytes= and
+    hbm_write_bytes= in its kernel_metrics lines.
     """
-    path = REPO / "profiles" / f"{workload_tag}_traffic.txt"
+    path = profile_summary_path(workload_tag)
     if not path.exists():
         return None
     vals = {}
     for line in path.read_text().splitlines():
-        if "=" in line and not line.lstrip().startswith("#"):
-            k, v = line.split("=", 1)
-            vals[k.strip()] = v.strip()
-    try:
-        return int(vals["fetch_bytes"]) + int(vals["write_bytes"])
-    except (KeyError, ValueError):
+        for item in line.split(","):
+            if "=" in item:
+                key, val = item.strip().split("=", 1)
+                key = key.split(":")[-1].strip()
+                if key in ("hbm_read_bytes", "hbm_write_bytes"):
+                    try:
+                        vals[key] = float(val)
+                    except ValueError:
+                        pass
+    if len(vals) != 2:
         return None
+    return int(vals["hbm_read_bytes"] + vals["hbm_write_bytes"])
 
 
 def cpu_baseline(w, budget_s: float):
-    """Time the CPU oracle on whole heads of the workload until ~budget_s."""
-    import numpy as np
-    import torch
+    """The CPU oracle (numpy fp32 formula) over the whole workload on this host.
+
+    One untimed pass, then timed passes until `budget_s` is spent (at least
+    3, as many as fit); the median pass time is charged the same FLOP formula
+    as the GPU (causal halved, although the CPU computes every score).
+    """
     from oracle.attention_oracle import attention_ref
+    from flash_attn_npu_amd.workloads import make_inputs
 
     threads = len(os.sched_getaffinity(0))
     try:
@@ -71,34 +85,36 @@ def cpu_baseline(w, budget_s: float):
         limiter = threadpool_limits(limits=threads)
     except Exception:  # noqa: BLE001
         limiter = None
-    from flash_attn_npu_amd.workloads import make_inputs
-    q, k, v = make_inputs(w, device=None, batch_slice=slice(0, 1))
+    q, k, v = make_inputs(w)
     qn, kn, vn = (t.float().numpy() for t in (q, k, v))
-    # one warm-up head
-    attention_ref(qn[0, 0], kn[0, 0], vn[0, 0], w.causal, w.sm_scale, out_dtype="bfloat16")
-    heads = 0
-    t0 = time.perf_counter()
-    while heads < w.H and time.perf_counter() - t0 < budget_s:
-        attention_ref(qn[0, heads], kn[0, heads], vn[0, heads], w.causal, w.sm_scale,
-                      out_dtype="bfloat16")
-        heads += 1
-    elapsed = time.perf_counter() - t0
+    dt = "bfloat16" if "bf" in str(w.dtype) else "float16"
+
+    def one_pass():
+        t0 = time.perf_counter()
+        for b in range(w.B):
+            attention_ref(qn[b], kn[b], vn[b], w.causal, w.sm_scale, out_dtype=dt)
+        return time.perf_counter() - t0
+
+    first = one_pass()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start + first < budget_s and len(times) < 50):
+        times.append(one_pass())
     if limiter is not None:
         limiter.restore_original_limits()
-    flops = 4.0 * heads * w.S * w.S * w.D / (2.0 if w.causal else 1.0)
+    med = statistics.median(times)
     try:
         model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
     except Exception:  # noqa: BLE001
         model = "unknown"
     return {
-        "value": flops / elapsed / 1e12,
+        "value": w.flops / med / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{heads} of {w.B * w.H} (b,h) heads of the same workload (b=0), full S={w.S} "
-                  f"rows each, numpy fp32 oracle, {elapsed:.1f} s, charged the same causal-halved "
-                  f"FLOP formula; CPU: {model}",
-        "seconds_per_step_extrapolated": elapsed * (w.B * w.H) / max(heads, 1),
+        "sample": f"the whole workload ({w.B * w.H} heads, S={w.S}), numpy fp32 oracle, median of "
+                  f"{len(times)} timed passes after 1 warmup ({med:.2f} s/pass; every score computed, "
+                  f"charged the causal-halved FLOP formula); CPU: {model}",
     }
 
 
@@ -107,8 +123,11 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup-seconds", type=float, default=1.0)
     ap.add_argument("--config", type=int, default=2, help="1-based index of the measured configuration")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="after timing, run a plain 256 MiB device copy (rocprofv3 FETCH/WRITE calibration)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -135,9 +154,17 @@ def main(argv=None):
     def step():
         return fa.attention(q, k, v, w.causal, w.sm_scale, return_lse=w.with_lse)
 
-    for _ in range(args.warmup):
+    # Warm up for at least W steps and at least one second, so the timed steps
+    # run at the clocks a sustained load settles at.
+    t_w = time.perf_counter()
+    n_w = 0
+    while n_w < args.warmup or time.perf_counter() - t_w < args.warmup_seconds:
         step()
+        n_w += 1
+        if n_w % 10 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
+    log(f"warmup: {n_w} steps in {time.perf_counter() - t_w:.2f} s")
 
     stream = torch.cuda.current_stream()
     ev0 = torch.cuda.Event(enable_timing=True)
@@ -151,6 +178,18 @@ def main(argv=None):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ev_ms = ev0.elapsed_time(ev1)
+
+    # Per-launch spread from events around single launches.
+    per = []
+    for _ in range(10):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) * 1e3)
+    log(f"single-launch events: min {min(per):.1f} median {statistics.median(per):.1f} max {max(per):.1f} us")
 
     # Evaluator-style per-call wall clock (perf_counter around call + synchronize,
     # evaluate_attention.py:233-264), for comparison only.
@@ -168,6 +207,14 @@ def main(argv=None):
     log(f"wall {ms_per_step * 1e3:.1f} us/step, events {kernel_ms * 1e3:.1f} us/launch, "
         f"evaluator-style median {statistics.median(samples):.1f} us")
     log(f"HBM-level algorithmic bytes {w.io_bytes} -> {w.io_bytes / (kernel_ms * 1e-3) / 1e9:.0f} GB/s")
+
+    if args.calibrate_copy:
+        a = torch.empty(128 * 1024 * 1024, dtype=torch.float16, device="cuda").fill_(1.0)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
 
     tag = w.name
     traffic = read_traffic(tag)

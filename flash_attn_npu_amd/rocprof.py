@@ -1,0 +1,219 @@
+"""rocprofv3 counter passes and the profile_summary.{json,txt} emitter.
+
+MI355X counterpart of the reference's in-module profiling
+(flash_attention_forward.py:255-613, 1204-1296): there, torch_npu's profiler
+runs one pass per AiC metric and the CSVs are folded into
+`profile_summary.json` / `profile_summary.txt` (write_profile_summary_files,
+:436-522), which `compare_results_plus.py` (:274-367) reads.  Here each pass
+is a `rocprofv3` subprocess (counters collected in their own runs, at most the
+per-block hardware limits per pass), and the result folds into the same
+schema, one entry per pass:
+
+    {pass_name: {"profiler_output", "op_name", "op": {...}, "kernel": {...},
+                 "kernel_columns": [...], "step": {}, "api": {...},
+                 "l2": {...}, "l2_columns": [...]}}
+
+so `python compare_results_plus.py A/profile_summary.json B/profile_summary.json`
+compares two MI355X runs unmodified.
+
+    python -m flash_attn_npu_amd.rocprof run --out result_dir -- python3 bench.py --steps 5 --cpu-seconds 0
+    python -m flash_attn_npu_amd.rocprof summarize result_dir
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import os
+import statistics
+import subprocess
+import sys
+from pathlib import Path
+
+PROFILE_OP_NAME = "fa_fwd"
+
+# One entry per rocprofv3 run.  None = kernel trace only.  Each counter list
+# fits one pass (<= 8 SQ, <= 4 TCC (FETCH_SIZE takes 3, WRITE_SIZE 2), <= 2 GRBM).
+METRIC_PLAN = {
+    "KernelTrace": None,
+    "Compute": ["SQ_WAVES", "SQ_BUSY_CYCLES", "SQ_WAVE_CYCLES", "SQ_INSTS_VALU", "SQ_INSTS_MFMA",
+                "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_ACTIVE_INST_VALU", "SQ_INSTS_SALU", "GRBM_GUI_ACTIVE"],
+    "LDS": ["SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_WAIT_INST_LDS",
+            "SQ_ACTIVE_INST_LDS", "SQ_VALU_MFMA_COEXEC_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY"],
+    "L2": ["TCC_HIT_sum", "TCC_MISS_sum"],
+    "HBMRead": ["FETCH_SIZE"],
+    "HBMWrite": ["WRITE_SIZE"],
+}
+
+# gfx950: 256 CUs x 4 SIMDs; one v_mfma_f32_32x32x16 keeps a SIMD's matrix
+# core busy for 32 cycles (SQ_VALU_MFMA_BUSY_CYCLES counts those cycles).
+NUM_SIMDS = 1024
+COPY_BYTES = 256 * 1024 * 1024  # the calibration copy in bench.py --calibrate-copy
+
+
+def _read_csv(path: Path):
+    with path.open(newline="", encoding="utf-8") as f:
+        return list(csv.DictReader(f))
+
+
+def _is_target(name: str, op: str) -> bool:
+    return op in name
+
+
+def _is_copy(name: str) -> bool:
+    low = name.lower()
+    return "copy" in low or "elementwise" in low
+
+
+def _find(root: Path, suffix: str):
+    return sorted(root.rglob(f"*{suffix}"))
+
+
+def summarize_pass(pass_dir: Path, op: str = PROFILE_OP_NAME) -> dict:
+    """Fold one rocprofv3 output directory into one summary entry."""
+    entry = {"profiler_output": str(pass_dir), "op_name": op, "op": {}, "kernel": {},
+             "kernel_columns": [], "step": {}, "api": {}, "l2": {}, "l2_columns": []}
+    traces = _find(pass_dir, "kernel_trace.csv")
+    durations, all_total = [], 0.0
+    for tr in traces:
+        for r in _read_csv(tr):
+            d = (float(r["End_Timestamp"]) - float(r["Start_Timestamp"])) / 1e3
+            all_total += d
+            if _is_target(r["Kernel_Name"], op):
+                durations.append(d)
+                entry["op"]["OP Type"] = r["Kernel_Name"]
+                entry["kernel"]["Block Num"] = float(r["Grid_Size_X"]) / float(r["Workgroup_Size_X"])
+                entry["kernel"]["LDS_Block_Size"] = float(r["LDS_Block_Size"])
+                entry["kernel"]["VGPR_Count"] = float(r.get("VGPR_Count", 0) or 0)
+                entry["kernel"]["Scratch_Size"] = float(r.get("Scratch_Size", 0) or 0)
+    if durations:
+        entry["op"].update({
+            "Core Type": "MI355X gfx950",
+            "Count": float(len(durations)),
+            "Total Time(us)": sum(durations),
+            "Min Time(us)": min(durations),
+            "Avg Time(us)": statistics.mean(durations),
+            "Max Time(us)": max(durations),
+            "Ratio(%)": 100.0 * sum(durations) / all_total if all_total else None,
+        })
+        entry["kernel"]["Duration(us)"] = statistics.mean(durations)
+        entry["kernel"]["kernel_count"] = float(len(durations))
+
+    counters: dict[str, list[float]] = {}
+    copy_counters: dict[str, list[float]] = {}
+    for cc in _find(pass_dir, "counter_collection.csv"):
+        for r in _read_csv(cc):
+            dst = counters if _is_target(r["Kernel_Name"], op) else (
+                copy_counters if _is_copy(r["Kernel_Name"]) else None)
+            if dst is not None:
+                dst.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    k = entry["kernel"]
+    for name, vals in counters.items():
+        k[name] = statistics.mean(vals)
+    # Derived figures.
+    if "SQ_VALU_MFMA_BUSY_CYCLES" in k and "GRBM_GUI_ACTIVE" in k and k["GRBM_GUI_ACTIVE"]:
+        # GRBM_GUI_ACTIVE sums the 8 XCDs' busy cycles.
+        k["MfmaUtil(%)"] = 100.0 * k["SQ_VALU_MFMA_BUSY_CYCLES"] / NUM_SIMDS / (k["GRBM_GUI_ACTIVE"] / 8)
+    if "SQ_LDS_BANK_CONFLICT" in k and k.get("SQ_LDS_IDX_ACTIVE"):
+        k["LDSBankConflict(%)"] = 100.0 * k["SQ_LDS_BANK_CONFLICT"] / k["SQ_LDS_IDX_ACTIVE"]
+    for cname, label in (("FETCH_SIZE", "hbm_read_bytes"), ("WRITE_SIZE", "hbm_write_bytes")):
+        if cname in k:
+            factor = 1.0
+            if copy_counters.get(cname):
+                factor = COPY_BYTES / (statistics.mean(copy_counters[cname]) * 1024.0)
+                k[f"{cname}_copy_factor"] = factor
+            k[label] = k[cname] * 1024.0 * factor
+    if "TCC_HIT_sum" in k and "TCC_MISS_sum" in k:
+        tot = k["TCC_HIT_sum"] + k["TCC_MISS_sum"]
+        entry["l2"] = {"l2_count": 1.0, "Hit Rate": k["TCC_HIT_sum"] / tot if tot else None}
+        entry["l2_columns"] = ["Hit Rate"]
+    entry["kernel_columns"] = [c for c in k if c != "kernel_count"]
+    entry["api"] = {"launch": {"Count": entry["op"].get("Count")}}
+    return entry
+
+
+def write_profile_summary_files(root: Path, summary_by_metric: dict):
+    """profile_summary.json + profile_summary.txt, as flash_attention_forward.py:436-522."""
+    root = Path(root)
+    root.mkdir(parents=True, exist_ok=True)
+    json_path = root / "profile_summary.json"
+    txt_path = root / "profile_summary.txt"
+    json_path.write_text(json.dumps(summary_by_metric, indent=2))
+    lines = []
+    for metric, s in summary_by_metric.items():
+        op = s.get("op", {})
+        lines.append(f"[{metric}]")
+        lines.append(f"profiler_output={s.get('profiler_output')}")
+        lines.append("op: type={}, count={}, avg_us={}, min_us={}, max_us={}, ratio_pct={}".format(
+            op.get("OP Type", "n/a"), _fmt(op.get("Count")), _fmt(op.get("Avg Time(us)")),
+            _fmt(op.get("Min Time(us)")), _fmt(op.get("Max Time(us)")), _fmt(op.get("Ratio(%)"))))
+        if s.get("kernel_columns"):
+            lines.append("kernel_metrics: " + ", ".join(
+                f"{c}={_fmt(s['kernel'].get(c))}" for c in s["kernel_columns"]))
+        if s.get("l2_columns"):
+            lines.append("l2_cache: " + ", ".join(f"{c}={_fmt(s['l2'].get(c), 6)}" for c in s["l2_columns"]))
+        lines.append("")
+    txt_path.write_text("\n".join(lines).rstrip() + "\n")
+    return json_path, txt_path
+
+
+def _fmt(v, precision=3):
+    if v is None:
+        return "n/a"
+    if isinstance(v, str):
+        return v
+    return f"{v:.{precision}f}"
+
+
+def run_passes(out: Path, target: list[str], plan=None, timeout=120) -> dict:
+    """Run one rocprofv3 process per pass of `plan` over the command `target`."""
+    plan = METRIC_PLAN if plan is None else plan
+    out = Path(out).resolve()
+    out.mkdir(parents=True, exist_ok=True)
+    env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
+    summary = {}
+    for name, counters in plan.items():
+        pdir = out / name
+        cmd = ["rocprofv3"]
+        cmd += ["--kernel-trace", "--stats"] if counters is None else ["--pmc", *counters]
+        cmd += ["-d", str(pdir), "-o", "run", "--output-format", "csv", "--", *target]
+        print(f"[rocprof] pass {name}: {' '.join(cmd)}", flush=True)
+        proc = subprocess.run(cmd, env=env, cwd="/tmp", timeout=timeout, capture_output=True, text=True)
+        (out / f"{name}.log").write_text(proc.stdout + proc.stderr)
+        if proc.returncode != 0:
+            raise RuntimeError(f"rocprofv3 pass {name} failed ({proc.returncode}); see {out / (name + '.log')}")
+        summary[name] = summarize_pass(pdir)
+    return summary
+
+
+def summarize_dir(out: Path, plan=None) -> dict:
+    plan = METRIC_PLAN if plan is None else plan
+    return {name: summarize_pass(Path(out) / name) for name in plan if (Path(out) / name).exists()}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    r = sub.add_parser("run", help="run every counter pass over a command, then summarize")
+    r.add_argument("--out", required=True)
+    r.add_argument("--passes", default=",".join(METRIC_PLAN), help="comma-separated subset of the plan")
+    r.add_argument("target", nargs=argparse.REMAINDER)
+    s = sub.add_parser("summarize", help="fold existing pass directories into profile_summary.*")
+    s.add_argument("out")
+    args = ap.parse_args(argv)
+    if args.cmd == "run":
+        target = args.target[1:] if args.target and args.target[0] == "--" else args.target
+        if not target:
+            ap.error("missing target command after --")
+        plan = {k: METRIC_PLAN[k] for k in args.passes.split(",")}
+        summary = run_passes(Path(args.out), target, plan)
+    else:
+        summary = summarize_dir(Path(args.out))
+    j, t = write_profile_summary_files(Path(args.out), summary)
+    print(t.read_text())
+    print(f"wrote {j} and {t}")
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,261 @@
+"""CPU: the C-ABI library and the drop-in module's host logic (no GPU needed).
+
+The library must load, export every function include/fa_fwd.h declares, and
+answer the host-only calls (fa_validate, fa_query_config, fa_kernel_info,
+fa_error_string, fa_abi_version, fa_params_size) without touching a GPU.  The
+Python layer must reproduce the reference's argument checks and tiling API
+(flash_attention_forward.py:156-252, 616-644, 1114-1122).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+
+from flash_attn_npu_amd import flash_attention_forward as fa
+from flash_attn_npu_amd import workloads as W
+
+REPO = Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "fa_fwd.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return fa._load_library()
+
+
+def header_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(fa_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_function(lib):
+    names = header_functions()
+    assert {"fa_fwd", "fa_validate", "fa_query_config", "fa_error_string", "fa_abi_version",
+            "fa_num_kernels", "fa_kernel_info", "fa_params_size"} <= set(names)
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_exported_symbols_in_dynamic_table():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(fa.library_path())], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (fa_\w+)", out))
+    assert set(header_functions()) <= exported
+
+
+def test_abi_version_and_struct_layout(lib):
+    assert lib.fa_abi_version() == 1
+    assert lib.fa_params_size() == ctypes.sizeof(fa.FaFwdParams) == 216
+
+
+def _params(**kw):
+    p = fa.FaFwdParams()
+    B, H, S, D = kw.get("shape", (1, 2, 128, 64))
+    # Fake but 16-byte-aligned device addresses: fa_validate never dereferences them.
+    base = 1 << 40
+    p.q, p.k, p.v, p.o = base, base + (1 << 30), base + (2 << 30), base + (3 << 30)
+    p.lse = kw.get("lse", base + (4 << 30))
+    for arr in (p.q_stride, p.k_stride, p.v_stride, p.o_stride):
+        arr[0], arr[1], arr[2], arr[3] = H * S * D, S * D, D, 1
+    p.B, p.H, p.Sq, p.Sk, p.D = B, H, S, S, D
+    p.dtype = kw.get("dtype", 1)
+    p.causal = kw.get("causal", 1)
+    p.sm_scale = kw.get("scale", 0.125)
+    p.block_m, p.block_n = kw.get("bm", 0), kw.get("bn", 0)
+    p.num_programs = kw.get("programs", 0)
+    return p
+
+
+def test_validate_accepts_good_params(lib):
+    assert lib.fa_validate(ctypes.byref(_params())) == 0
+    assert lib.fa_validate(ctypes.byref(_params(lse=None))) == 0
+    assert lib.fa_validate(ctypes.byref(_params(shape=(0, 4, 128, 128)))) == 0  # empty is fine
+
+
+@pytest.mark.parametrize("mutate,code", [
+    (lambda p: setattr(p, "q", None), -1),
+    (lambda p: setattr(p, "Sq", -1), -2),
+    (lambda p: setattr(p, "Sk", 0), -2),
+    (lambda p: setattr(p, "D", 96), -3),
+    (lambda p: setattr(p, "dtype", 7), -4),
+    (lambda p: p.k_stride.__setitem__(3, 2), -5),
+    (lambda p: p.v_stride.__setitem__(2, 12), -5),
+    (lambda p: p.o_stride.__setitem__(2, 8), -5),       # seq stride below D
+    (lambda p: setattr(p, "o", (1 << 40) + 8), -6),
+    (lambda p: setattr(p, "block_m", 128), -7),          # BM without BN
+    (lambda p: (setattr(p, "block_m", 96), setattr(p, "block_n", 64)), -7),
+    (lambda p: setattr(p, "sm_scale", float("nan")), -8),
+    (lambda p: setattr(p, "sm_scale", float("inf")), -8),
+    (lambda p: setattr(p, "num_programs", -3), -9),
+])
+def test_validate_rejects(lib, mutate, code):
+    p = _params()
+    mutate(p)
+    assert lib.fa_validate(ctypes.byref(p)) == code
+    assert lib.fa_error_string(code) != b"unknown fa_fwd status"
+
+
+def test_validate_rejects_slices_over_2gib(lib):
+    p = _params(shape=(1, 1, 9_000_000, 128))  # 9e6 rows x 256 B > 2 GiB
+    assert lib.fa_validate(ctypes.byref(p)) == -2
+
+
+def test_error_strings(lib):
+    assert lib.fa_error_string(0) == b"ok"
+    assert lib.fa_error_string(-100).startswith(b"the HIP runtime")
+    assert lib.fa_error_string(12345) == b"unknown fa_fwd status"
+
+
+def test_query_config_headline(lib):
+    out = (ctypes.c_int32 * 8)()
+    assert lib.fa_query_config(ctypes.byref(_params(shape=(4, 32, 2048, 128))), out) == 0
+    bm, bn, waves, grid, tiles, lds, stage, kid = list(out)
+    assert (bm, bn) == tuple(fa.get_tiling(4, 32, 2048, 128, True))
+    assert waves == bm // 32 and tiles == math.ceil(2048 / bm) * 128 and grid == tiles
+    assert stage == 3 and 0 < lds <= 160 * 1024 and 0 <= kid < lib.fa_num_kernels()
+
+
+def test_query_config_persistent_cap(lib):
+    out = (ctypes.c_int32 * 8)()
+    assert lib.fa_query_config(ctypes.byref(_params(shape=(4, 32, 2048, 128), programs=20)), out) == 0
+    assert out[3] == 20
+
+
+def test_kernel_table_is_consistent(lib):
+    rows = fa.kernel_table()
+    assert rows, "library has no kernels"
+    seen = set()
+    for r in rows:
+        assert r["HEAD_DIM"] in fa.SUPPORTED_HEAD_DIMS
+        assert r["BLOCK_M"] == 32 * r["waves"] and r["BLOCK_N"] % 32 == 0
+        seen.add((r["HEAD_DIM"], r["dtype"], r["causal"]))
+    for d in fa.SUPPORTED_HEAD_DIMS:
+        for dt in ("float16", "bfloat16"):
+            for c in (False, True):
+                assert (d, dt, c) in seen
+
+
+# ---------------------------------------------------------------------------
+# Python layer (the reference's module API)
+
+def test_module_surface():
+    for name in ("DEVICE", "attention", "flash_attention_forward", "_launch_kernel", "get_tiling",
+                 "get_tiling_source", "_describe_runtime", "_get_persistent_programs", "_make_inputs",
+                 "_validate_inputs", "_resolve_tiling", "PROFILE_OP_NAME", "DEFAULT_TILING_PRESETS"):
+        assert hasattr(fa, name), name
+    assert fa.DEVICE == "cuda"
+    assert fa.flash_attention_forward is fa.attention
+
+
+def test_module_loads_by_path():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("flash_attention_candidate",
+                                                  REPO / "flash_attn_npu_amd" / "flash_attention_forward.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    assert mod.DEVICE == "cuda" and callable(mod.attention)
+    assert mod._load_library().fa_abi_version() == 1
+
+
+@pytest.mark.parametrize("shapes,msg", [
+    (((2, 3, 4), (2, 3, 4), (2, 3, 4)), "4D"),
+    (((1, 2, 8, 64), (1, 2, 9, 64), (1, 2, 8, 64)), "same shape"),
+    (((1, 2, 8, 48), (1, 2, 8, 48), (1, 2, 8, 48)), "HEAD_DIM must be one of"),
+    (((1, 2, 8, 256), (1, 2, 8, 256), (1, 2, 8, 256)), "not supported by this build"),
+])
+def test_validate_inputs_like_reference(shapes, msg):
+    q, k, v = (torch.zeros(s, dtype=torch.float16) for s in shapes)
+    with pytest.raises(ValueError, match=msg):
+        fa._validate_inputs(q, k, v)
+
+
+def test_rejects_cpu_tensors_and_bad_dtype():
+    q = torch.zeros((1, 2, 8, 64), dtype=torch.float16)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        fa.attention(q, q, q, False, 0.1)
+    q32 = torch.zeros((1, 2, 8, 64), dtype=torch.float32)
+    with pytest.raises(ValueError, match="float16"):
+        fa.attention(q32, q32, q32, False, 0.1)
+
+
+def test_tiling_resolution(monkeypatch):
+    with pytest.raises(ValueError, match="together"):
+        fa._resolve_tiling(1, 1, 128, 64, False, bm=128)
+    assert fa._resolve_tiling(1, 1, 128, 64, False, bm=256, bn=64) == (256, 64, "override")
+    monkeypatch.setitem(fa.DEFAULT_TILING_PRESETS, (2, 3, 4096, 128, True), (256, 64))
+    assert fa.get_tiling(2, 3, 4096, 128, True) == (256, 64)
+    assert fa.get_tiling_source(2, 3, 4096, 128, True) == "preset"
+    assert fa.get_tiling_source(2, 3, 4097, 128, True) == "fallback"
+
+
+def test_persistent_programs_env(monkeypatch):
+    monkeypatch.delenv("PERSISTENT_PROGRAMS", raising=False)
+    assert fa._get_persistent_programs() == fa.DEFAULT_PERSISTENT_PROGRAMS
+    monkeypatch.setenv("PERSISTENT_PROGRAMS", "64")
+    assert fa._get_persistent_programs() == 64
+    monkeypatch.setenv("PERSISTENT_PROGRAMS", "0")
+    with pytest.raises(ValueError):
+        fa._get_persistent_programs()
+
+
+def test_describe_runtime_keys(monkeypatch):
+    monkeypatch.delenv("PERSISTENT_PROGRAMS", raising=False)
+    rt = fa._describe_runtime(4, 32, 2048, 128, True)
+    assert set(rt) >= {"selected_config", "tiling_source", "total_tiles", "launched_programs", "stage"}
+    assert rt["stage"] == 3 and rt["launched_programs"] == rt["total_tiles"]
+    assert fa._describe_runtime(4, 32, 2048, 128, False)["stage"] == 1
+
+
+def test_check_maps_errors():
+    with pytest.raises(ValueError):
+        fa._check(-5, "x")
+    with pytest.raises(RuntimeError):
+        fa._check(-100, "x")
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(fa, "_LIB", None)
+    monkeypatch.setenv("FA_MI355X_LIB", str(tmp_path / "nope.so"))
+    with pytest.raises(RuntimeError, match="no fallback"):
+        fa._load_library()
+
+
+# ---------------------------------------------------------------------------
+# Workloads and bench contract
+
+def test_workload_inputs_are_seeded():
+    w = W.CONFIGS[0]
+    a = W.make_inputs(w)
+    b = W.make_inputs(w)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y) and x.dtype == w.dtype and x.shape == (w.B, w.H, w.S, w.D)
+
+
+def test_ragged_config_distributions():
+    w = W.CONFIGS[4]
+    q, k, v = W.make_inputs(w, batch_slice=slice(0, 1))
+    assert float(v.float().abs().max()) <= 1.0
+    frac_big = float((q.float().abs() > 4.5).float().mean())
+    assert 0.003 < frac_big < 0.02  # ~1% of entries scaled x8
+    assert w.S % 64 != 0 and w.causal and w.dtype == torch.bfloat16
+
+
+def test_configs_match_task():
+    shapes = [(c.B, c.H, c.S, c.D, c.causal) for c in W.CONFIGS]
+    assert shapes == [(1, 8, 512, 64, False), (4, 32, 2048, 128, True), (2, 16, 8192, 128, True),
+                      (16, 16, 1024, 64, False), (8, 32, 3000, 128, True)]
+    assert W.HEADLINE.flops == pytest.approx(1.3744e11, rel=1e-4)
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, str(REPO / "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=60)
+    assert r.returncode == 2 and "one GPU" in r.stderr

@@ -1,0 +1,251 @@
+"""CPU: pin the oracle (oracle/attention_oracle.py).
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped
+scale, the mask shifted by one, a transposed operand, a missing max
+subtraction, the LSE in base 2) fails at least one of them; the mutant tests at
+the end plant exactly those mistakes in copies of the oracle and assert that
+the pins reject them.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import scipy.special
+
+from oracle.attention_oracle import (
+    attention_bruteforce,
+    attention_flops,
+    attention_ref,
+    round_bf16,
+    round_fp16,
+)
+
+RNG = np.random.default_rng(20261201)
+
+
+def rand(*shape, scale=1.0):
+    return (RNG.standard_normal(shape) * scale).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# Pins, written against a generic oracle `fn(q, k, v, causal, scale) -> (o, lse)`.
+
+def pin_bruteforce(fn, tol=2e-5):
+    for sq, d, causal in [(1, 8, False), (5, 8, True), (17, 16, False), (17, 16, True), (37, 64, True)]:
+        q, k, v = rand(sq, d), rand(sq, d), rand(sq, d)
+        o, lse = fn(q, k, v, causal, 0.37)
+        ob, lb = attention_bruteforce(q, k, v, causal, 0.37)
+        if not (np.abs(o - ob).max() <= tol and np.abs(lse - lb).max() <= tol):
+            return False
+    # Sq != Sk non-causal (rectangular)
+    q, k, v = rand(3, 8), rand(11, 8), rand(11, 8)
+    o, lse = fn(q, k, v, False, 0.5)
+    ob, lb = attention_bruteforce(q, k, v, False, 0.5)
+    return np.abs(o - ob).max() <= tol and np.abs(lse - lb).max() <= tol
+
+
+def pin_zero_keys(fn):
+    """K = 0: every visible logit is 0, so weights are uniform.
+
+    Non-causal: O = mean(V), LSE = ln(Sk).  Causal row i: O_i = mean(V[:i+1]),
+    LSE_i = ln(i + 1).
+    """
+    s, d = 23, 16
+    q, k, v = rand(s, d), np.zeros((s, d), np.float32), rand(s, d)
+    o, lse = fn(q, k, v, False, 0.9)
+    ok = np.allclose(o, np.broadcast_to(v.mean(0), o.shape), atol=1e-5)
+    ok &= np.allclose(lse, math.log(s), atol=1e-5)
+    o, lse = fn(q, k, v, True, 0.9)
+    want = np.cumsum(v, 0) / np.arange(1, s + 1)[:, None]
+    ok &= np.allclose(o, want, atol=1e-5)
+    ok &= np.allclose(lse, np.log(np.arange(1, s + 1)), atol=1e-5)
+    return bool(ok)
+
+
+def pin_first_causal_row(fn):
+    """Causal row 0 sees only key 0: O_0 = V_0 and LSE_0 = scale * q_0 . k_0."""
+    q, k, v = rand(9, 32), rand(9, 32), rand(9, 32)
+    o, lse = fn(q, k, v, True, 0.21)
+    return bool(np.allclose(o[0], v[0], atol=1e-6) and abs(lse[0] - 0.21 * float(q[0] @ k[0])) <= 1e-5)
+
+
+def pin_shift(fn):
+    """Adding c to every logit leaves O unchanged and raises LSE by c.
+
+    The shift is built into the operands: q' = [q, 1], k' = [k, c / scale].
+    """
+    s, d, scale, c = 19, 16, 0.3, 2.5
+    q, k, v = rand(s, d), rand(s, d), rand(s, d)
+    q2 = np.concatenate([q, np.ones((s, 1), np.float32)], 1)
+    k2 = np.concatenate([k, np.full((s, 1), c / scale, np.float32)], 1)
+    ok = True
+    for causal in (False, True):
+        o1, l1 = fn(q, k, v, causal, scale)
+        o2, l2 = fn(q2, k2, v, causal, scale)
+        ok &= np.allclose(o1, o2, atol=1e-5) and np.allclose(l2 - l1, c, atol=1e-4)
+    return bool(ok)
+
+
+def pin_one_hot(fn):
+    """One-hot q_i = e_{p(i)}, k_j = e_j with a large scale: row i selects V[p(i)]."""
+    s = 12
+    perm = RNG.permutation(s)
+    q = np.eye(s, dtype=np.float32)[perm]
+    k = np.eye(s, dtype=np.float32)
+    v = rand(s, 8)
+    o, lse = fn(q, k, v, False, 60.0)
+    return bool(np.allclose(o, v[perm], atol=1e-5) and np.allclose(lse, 60.0, atol=1e-4))
+
+
+def pin_causal_prefix(fn):
+    """Causal row i equals non-causal attention of q_i over keys [0, i]."""
+    s, d = 14, 16
+    q, k, v = rand(s, d), rand(s, d), rand(s, d)
+    o, lse = fn(q, k, v, True, 0.4)
+    for i in (0, 3, 9, 13):
+        oi, li = fn(q[i:i + 1], k[:i + 1], v[:i + 1], False, 0.4)
+        if not (np.allclose(o[i], oi[0], atol=1e-6) and abs(lse[i] - li[0]) <= 1e-6):
+            return False
+    return True
+
+
+def pin_library(fn):
+    """scipy.special.softmax / logsumexp (an independent implementation) on the logits."""
+    s, d = 31, 64
+    q, k, v = rand(s, d), rand(s, d), rand(s, d)
+    logits = (q.astype(np.float64) @ k.astype(np.float64).T) * 0.125
+    logits[np.triu_indices(s, 1)] = -np.inf
+    o, lse = fn(q, k, v, True, 0.125)
+    want_o = scipy.special.softmax(logits, axis=-1) @ v.astype(np.float64)
+    want_l = scipy.special.logsumexp(logits, axis=-1)
+    return bool(np.allclose(o, want_o, atol=2e-5) and np.allclose(lse, want_l, atol=2e-5))
+
+
+def pin_large_logits(fn):
+    """Logits far beyond exp's range (|s| ~ 1e3): the max-subtraction must keep it finite."""
+    s, d = 16, 8
+    q, k, v = rand(s, d) * 30, rand(s, d) * 30, rand(s, d)
+    o, lse = fn(q, k, v, False, 1.0)
+    ob, lb = attention_bruteforce(q, k, v, False, 1.0)
+    return bool(np.isfinite(o).all() and np.allclose(o, ob, atol=1e-4) and np.allclose(lse, lb, rtol=1e-6))
+
+
+PINS = [pin_bruteforce, pin_zero_keys, pin_first_causal_row, pin_shift, pin_one_hot,
+        pin_causal_prefix, pin_library, pin_large_logits]
+
+
+def oracle(q, k, v, causal, scale):
+    return attention_ref(q, k, v, causal, scale)
+
+
+@pytest.mark.parametrize("pin", PINS, ids=[p.__name__ for p in PINS])
+def test_oracle_pins(pin):
+    assert pin(oracle)
+
+
+# ---------------------------------------------------------------------------
+# Mutants: each plants one plausible mistake; at least one pin must reject it.
+
+def _mutant_no_scale(q, k, v, causal, scale):
+    return attention_ref(q, k, v, causal, 1.0)
+
+
+def _mutant_mask_off_by_one(q, k, v, causal, scale):
+    # Masks the diagonal as well (triu with k=0): row 0 would see no key at all,
+    # so emulate "j < i" visibility plus key 0 for row 0.
+    q = np.asarray(q, np.float32)
+    o, lse = attention_ref(q, k, v, False, scale)
+    if not causal:
+        return o, lse
+    s = q.shape[0]
+    out = np.empty_like(o)
+    lo = np.empty_like(lse)
+    for i in range(s):
+        hi = max(i, 1)
+        oi, li = attention_ref(q[i:i + 1], k[:hi], v[:hi], False, scale)
+        out[i], lo[i] = oi[0], li[0]
+    return out, lo
+
+
+def _mutant_transposed_scores(q, k, v, causal, scale):
+    # Uses K Q^T instead of Q K^T (scores transposed) before the softmax.
+    q = np.asarray(q, np.float32)
+    k = np.asarray(k, np.float32)
+    if q.shape[0] != k.shape[0]:
+        return attention_ref(q, k, v, causal, scale)
+    s = (k @ q.T) * scale
+    if causal:
+        s = np.where(np.triu(np.ones_like(s, bool), 1), -np.inf, s)
+    m = s.max(-1, keepdims=True)
+    e = np.exp(s - m)
+    return (e / e.sum(-1, keepdims=True)) @ v, (np.log(e.sum(-1)) + m[:, 0]).astype(np.float32)
+
+
+def _mutant_lse_base2(q, k, v, causal, scale):
+    o, lse = attention_ref(q, k, v, causal, scale)
+    return o, lse / np.float32(math.log(2.0))
+
+
+def _mutant_unstable(q, k, v, causal, scale):
+    # No max subtraction (the reference's "lazy" path, flash_attention_forward.py:725-752).
+    q = np.asarray(q, np.float32)
+    s = (q @ np.asarray(k, np.float32).T) * np.float32(scale)
+    if causal:
+        s = np.where(np.triu(np.ones_like(s, bool), 1), -np.inf, s)
+    with np.errstate(over="ignore", invalid="ignore"):
+        e = np.exp(s)
+        return (e / e.sum(-1, keepdims=True)) @ v, np.log(e.sum(-1)).astype(np.float32)
+
+
+MUTANTS = [_mutant_no_scale, _mutant_mask_off_by_one, _mutant_transposed_scores,
+           _mutant_lse_base2, _mutant_unstable]
+
+
+@pytest.mark.parametrize("mutant", MUTANTS, ids=[m.__name__ for m in MUTANTS])
+def test_pins_reject_mutant(mutant):
+    with np.errstate(all="ignore"):
+        results = [pin(mutant) for pin in PINS]
+    assert not all(results), f"{mutant.__name__} passed every pin"
+
+
+# ---------------------------------------------------------------------------
+# Rounding helpers and shape handling.
+
+def test_round_bf16_matches_torch():
+    torch = pytest.importorskip("torch")
+    x = np.concatenate([rand(4096) * 10, np.array([0.0, -0.0, 1.0, 1.00390625, 1.005859375, 3.0e38,
+                                                   -3.0e38, 1e-40, np.inf, -np.inf], np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(round_bf16(x), want)
+    assert np.isnan(round_bf16(np.array([np.nan], np.float32)))[0]
+
+
+def test_round_fp16_matches_torch():
+    torch = pytest.importorskip("torch")
+    x = rand(4096) * 100
+    want = torch.from_numpy(x).to(torch.float16).float().numpy()
+    np.testing.assert_array_equal(round_fp16(x), want)
+
+
+def test_batched_shapes_and_rounding():
+    q, k, v = rand(2, 3, 20, 16), rand(2, 3, 20, 16), rand(2, 3, 20, 16)
+    o, lse = attention_ref(q, k, v, True, 0.25, out_dtype="bfloat16")
+    assert o.shape == (2, 3, 20, 16) and lse.shape == (2, 3, 20)
+    o1, l1 = attention_ref(q[1, 2], k[1, 2], v[1, 2], True, 0.25)
+    np.testing.assert_array_equal(o[1, 2], round_bf16(o1))
+    np.testing.assert_allclose(lse[1, 2], l1, atol=1e-6)
+
+
+def test_flops_formula():
+    assert attention_flops(4, 32, 2048, 2048, 128, True) == pytest.approx(1.3744e11, rel=1e-4)
+    assert attention_flops(1, 8, 512, 512, 64, False) == pytest.approx(5.369e8, rel=1e-3)
+
+
+def test_rejects_mismatched_shapes():
+    with pytest.raises(ValueError):
+        attention_ref(rand(4, 8), rand(4, 16), rand(4, 16), False, 1.0)
+    with pytest.raises(ValueError):
+        attention_ref(rand(2, 4, 8), rand(3, 4, 8), rand(3, 4, 8), False, 1.0)
