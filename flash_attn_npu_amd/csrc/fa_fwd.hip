@@ -62,13 +62,6 @@ constexpr float kLazyMaxThreshold = 8.0f;
 constexpr int kNumXcd = 8;
 constexpr int kMaxBlockM = 256;  // largest BLOCK_M of any kernel instance
 constexpr int kRowMargin = 1024; // rows addressed past a tensor's end (>= BLOCK_M, >= NR * BLOCK_N)
-#ifndef FA_FP16_DOT_SUM
-#define FA_FP16_DOT_SUM 1
-#endif
-constexpr bool kFp16DotSum = FA_FP16_DOT_SUM != 0;
-#ifndef FA_MFMA_PRIO
-#define FA_MFMA_PRIO 0
-#endif
 // FA_TIMING (development builds only): the ping-pong kernel accumulates, per
 // wave, the shader-clock cycles spent in each phase and writes them to
 // KernelArgs::timing.  The product build compiles none of it.
@@ -510,6 +503,9 @@ __device__ __forceinline__ void dma16(BufRsrc r, uint32_t lds_addr, uint32_t vof
 }
 #pragma clang diagnostic pop
 
+// s_waitcnt immediate: vmcnt(n), no wait on expcnt / lgkmcnt.
+constexpr int vmcnt_imm(int n) { return 0x0f70 | (n & 0xf) | ((n >> 4) << 14); }
+
 // sched_group_barrier masks.
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
@@ -529,7 +525,7 @@ struct Cfg2 {
   static_assert(CPR >= 8, "the swizzle needs at least 8 chunks per row");
   static_assert(IPT % NW == 0 && IPW >= 1, "DMA instructions must split evenly over waves");
   static_assert(BN % 32 == 0 && D % 32 == 0, "tile shape");
-  static_assert(NSTAGE >= 2 && NSTAGE <= 4, "stages");
+  static_assert(NSTAGE == 2, "double-buffered: one tile computes while the next lands");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one gfx950 CU");
 };
 
@@ -635,25 +631,23 @@ fa_fwd_dma_kernel(KernelArgs p) {
     float m_run = -INFINITY;
     float l_run = 0.f;
 
-    // One KV tile: wait for its DMA, barrier, refill the ring, then
+    // One KV tile: wait for its DMA, barrier, refill the other stage, then
     // S^T = K Q^T, online softmax, O^T += V^T P^T.  MASKED is a compile-time
     // switch: only tiles crossing the diagonal or the ragged key tail pay for
     // the mask (and for skipping tiles above a wave's own rows), and neither
-    // loop body branches on it.
-    auto kv_tile = [&](int t, auto masked_tag) {
+    // loop body branches on it.  STG = t % 2 is compile-time too, so every
+    // LDS read address is a per-lane base plus an immediate offset.
+    auto kv_tile = [&](int t, auto masked_tag, auto stage_tag) __attribute__((always_inline)) {
       constexpr bool MASKED = decltype(masked_tag)::value;
-      if (NSTAGE >= 3 && t + 1 < n_tiles) {
-        __builtin_amdgcn_s_waitcnt(0x0f70 | ((2 * C::IPW) & 0xf) | (((2 * C::IPW) >> 4) << 14));
-      } else {
-        __builtin_amdgcn_s_waitcnt(0x0f70);
-      }
+      constexpr int STG = decltype(stage_tag)::value;
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
       __syncthreads();
-      if (t + NSTAGE - 1 < n_tiles) issue_tile(t + NSTAGE - 1);
+      if (t + 1 < n_tiles) issue_tile(t + 1);
 
       const int kbase = t * BN;
       if (MASKED && CAUSAL && kbase > wave_last_q) return;
 
-      const uint32_t st = (uint32_t)((t % NSTAGE) * C::STAGE);
+      constexpr uint32_t st = (uint32_t)(STG * C::STAGE);
 
       // S^T = K Q^T.  Fragment i = (s, kb); K fragments are read KPF ahead of
       // their MFMA, and the first VPF V^T fragments of the P*V product are
@@ -669,7 +663,6 @@ fa_fwd_dma_kernel(KernelArgs p) {
         const u32x2_t hi = lds_read_tr16(smem, vro[db][1] + imm + 8 * C::ROW);
         return (u32x4_t){lo[0], lo[1], hi[0], hi[1]};
       };
-      if (FA_MFMA_PRIO) __builtin_amdgcn_s_setprio(FA_MFMA_PRIO);
       u32x4_t kfr[NQK];
       u32x4_t vfr[NPV];
       f32x16_t sacc[BN / 32];
@@ -696,7 +689,6 @@ fa_fwd_dma_kernel(KernelArgs p) {
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * VPF, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, KPF, 0);
 
-      if (FA_MFMA_PRIO) __builtin_amdgcn_s_setprio(0);
       if (MASKED) {
         // Register r of block kb holds key kbase + 4h + (32kb + 8(r>>2) + (r&3));
         // it is visible iff that offset <= lim.
@@ -736,38 +728,21 @@ fa_fwd_dma_kernel(KernelArgs p) {
         for (int r = 0; r < 16; ++r) {
           const float pv = fast_exp2(__builtin_fmaf(sacc[kb][r], c, -mb));
           sacc[kb][r] = pv;
-          if (BF16 || !kFp16DotSum) lsum[r & 3] += pv;
+          lsum[r & 3] = (kb == 0 && r < 4) ? pv : lsum[r & 3] + pv;
         }
 
       // P^T fragments: k-step ks (16 keys) = registers 8t..8t+7 of block ks/2.
-      // fp16 P is also summed here, two rounded values per v_dot2_f32_f16
-      // (fp16 keeps 11 bits, far inside the LSE tolerance; bf16 keeps 8 and
-      // is summed in fp32 above instead).  The dot takes the f16x2 produced
-      // by the conversion itself: taking it back out of the packed dword with
-      // a bit_cast of a vector element is miscompiled by this toolchain (only
-      // element 0 survives).
       u32x4_t pf[BN / 16];
-      const f16x2_t ones_h = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
       for (int ks = 0; ks < BN / 16; ++ks) {
         const int kb = ks >> 1, t8 = (ks & 1) * 8;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const f32x2_t pair = {sacc[kb][t8 + 2 * w], sacc[kb][t8 + 2 * w + 1]};
-          if constexpr (BF16) {
-            pf[ks][w] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pair, bf16x2_t));
-          } else {
-            const f16x2_t hv = __builtin_convertvector(pair, f16x2_t);
-            pf[ks][w] = __builtin_bit_cast(uint32_t, hv);
-            if (kFp16DotSum) lsum[w] = __builtin_amdgcn_fdot2(hv, ones_h, lsum[w], false);
-          }
-        }
+        for (int w = 0; w < 4; ++w) pf[ks][w] = pack2<BF16>(sacc[kb][t8 + 2 * w], sacc[kb][t8 + 2 * w + 1]);
       }
       l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
 
       // O^T += V^T P^T; the A operand is two transpose reads (keys +0..3 and
       // +8..11 of the k-step), VPF fragments ahead of their MFMA.
-      if (FA_MFMA_PRIO) __builtin_amdgcn_s_setprio(FA_MFMA_PRIO);
 #pragma unroll
       for (int i = VPF; i < NPV; ++i) vfr[i] = vread(i);
 #pragma unroll
@@ -781,16 +756,26 @@ fa_fwd_dma_kernel(KernelArgs p) {
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
       }
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, VPF, 0);
-      if (FA_MFMA_PRIO) __builtin_amdgcn_s_setprio(0);
     };
 
-    // Tiles visible to every query of the workgroup need no mask.
+    // Tiles visible to every query of the workgroup need no mask.  Each run
+    // of tiles steps t in stage pairs (t even -> stage 0).
     int n_full = p.Sk / BN;
     if (CAUSAL) n_full = min(n_full, (q0 + 1) / BN);
     n_full = min(n_full, n_tiles);
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
     int t = 0;
-    for (; t < n_full; ++t) kv_tile(t, std::integral_constant<bool, false>{});
-    for (; t < n_tiles; ++t) kv_tile(t, std::integral_constant<bool, true>{});
+    auto run = [&](int end, auto masked_tag) __attribute__((always_inline)) {
+      if (t < end && (t & 1)) kv_tile(t++, masked_tag, S1{});
+      for (; t + 1 < end; t += 2) {
+        kv_tile(t, masked_tag, S0{});
+        kv_tile(t + 1, masked_tag, S1{});
+      }
+      if (t < end) kv_tile(t++, masked_tag, S0{});
+    };
+    run(n_full, std::integral_constant<bool, false>{});
+    run(n_tiles, std::integral_constant<bool, true>{});
 
     const float l_tot = halves_sum(l_run);
     const float inv = 1.f / l_tot;
@@ -851,9 +836,6 @@ struct Cfg3 {
   static_assert(NR >= 3 && NR <= 6, "ring depth");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one gfx950 CU");
 };
-
-// s_waitcnt immediate: vmcnt(n), no wait on expcnt / lgkmcnt.
-constexpr int vmcnt_imm(int n) { return 0x0f70 | (n & 0xf) | ((n >> 4) << 14); }
 
 template <int D, int BN, int NR, bool BF16, bool CAUSAL>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
