@@ -37,8 +37,10 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "fa_fwd.h"
@@ -59,7 +61,6 @@ constexpr float kLn2 = 0.6931471805599453f;
 // The running max only moves when a row max exceeds it by more than this many
 // log2 units, so un-normalised probabilities stay <= 2^8 (safe in fp16/bf16).
 constexpr float kLazyMaxThreshold = 8.0f;
-constexpr int kNumXcd = 8;
 constexpr int kMaxBlockM = 256;  // largest BLOCK_M of any kernel instance
 constexpr int kRowMargin = 1024; // rows addressed past a tensor's end (>= BLOCK_M, >= NR * BLOCK_N)
 // FA_TIMING (development builds only): the ping-pong kernel accumulates, per
@@ -83,8 +84,10 @@ struct KernelArgs {
   int32_t B, H, Sq, Sk;
   int32_t n_mtiles;     // ceil(Sq / BM)
   int32_t total_tiles;  // n_mtiles * B * H
-  int32_t xcd_remap;    // 1: grid == total_tiles, keep logical neighbours on one XCD
-  int32_t head_group;   // heads whose m-tiles are scheduled together (causal order)
+  unsigned long long *queue;  // this launch's tile-queue counters (see TileQueue)
+  int32_t nq;                 // tile queues: min(8, grid, B*H)
+  int32_t q_group;            // heads per group in a queue's order (>= 1)
+  int32_t q_bands;            // weight bands in a queue's order (>= 1)
   uint32_t q_sign;      // 0x80008000 when sm_scale < 0 (Q is negated in registers)
   float c;              // |sm_scale| * log2(e), > 0
   uint32_t *timing;     // per-wave phase cycle counts (FA_TIMING builds only), else null
@@ -162,40 +165,82 @@ __device__ __forceinline__ int vt_pos(int k) {
   return (k & ~15) | (pg << 2) | (k & 3);
 }
 
-// Logical tile index for workgroup `bid`.  When every tile has its own
-// workgroup, workgroups are dealt round-robin to the XCDs; renumber them so
-// that each XCD receives one contiguous run of logical tiles.
-__device__ __forceinline__ int logical_tile(int bid, int grid, int remap) {
-  if (!remap) return bid;
-  int x = bid % kNumXcd;
-  int base = grid / kNumXcd;
-  int extra = grid % kNumXcd;
-  // XCDs [0, extra) get base+1 workgroups, the rest get base.
-  int prefix = x * base + (x < extra ? x : extra);
-  return prefix + bid / kNumXcd;
-}
+// ---------------------------------------------------------------------------
+// Tile queues.
+//
+// Every kernel runs a persistent grid (as many workgroups as are resident at
+// once) that pulls (head, m-tile) tiles from nq = min(8, grid, B*H) queues:
+// workgroup b serves queue b % nq (the dispatcher sends workgroup b to XCD
+// b % 8, so a queue is an XCD's), and queue x owns heads x, x+nq, x+2nq, ...,
+// so a head's K/V is only ever read through one XCD's L2.  A queue hands out
+// its tiles heaviest first (causal: largest m-tile first, across its heads),
+// so the tail is made of the cheapest tiles.  Pulling instead of a static
+// split matters on gfx950: the two workgroups sharing a CU do not progress
+// at the same rate (the older one wins issue arbitration), so any fixed
+// assignment leaves one of them idle at the end.
+//
+// Ticket i of a queue is its i-th heaviest tile.  The queue's W workgroups
+// take tickets 0..W-1 statically (no atomic before the first tile); later
+// tickets come from a counter: ticket = W + atomicAdd(counter, 1), requested
+// at the top of a tile so its latency hides behind the tile.  Each of those
+// workgroups takes exactly one ticket past the end and stops, so the taker of
+// raw count n_tiles - 1 is the last user of the counter and resets it to 0:
+// the next launch (or a replay of this one) finds it clean.  The counters
+// live in a device array owned by the library, one group of kQueues per
+// launch slot (one 128-byte line per counter); launch slots rotate over
+// kQueueSlots, which bounds the launches that may be in flight on one device.
+constexpr int kQueues = 8;
+constexpr int kQueueSlots = 1024;
+constexpr int kQueueStride = 16;  // 128 bytes between counters
+__device__ unsigned long long g_tile_queues[kQueueSlots * kQueues * kQueueStride];
 
-// Logical tile -> (head index bh, m-tile).  Heads are taken in groups of
-// `group` (sized so that one group's m-tiles fill one XCD's workgroup slots):
-// the m-tiles of a group run together and share K/V through the XCD's L2.
-// Causal: inside a group, tiles go heaviest (largest m) first across the
-// group's heads, so the last workgroups dispatched are the cheapest ones.
-__device__ __forceinline__ void decode_tile(int L, int n_mtiles, int BH, int group, bool causal,
-                                            int *bh, int *mt) {
-  if (!causal || group <= 1) {
-    *bh = L / n_mtiles;
-    const int mr = L - *bh * n_mtiles;
-    *mt = causal ? (n_mtiles - 1 - mr) : mr;
-    return;
+struct TileQueue {
+  unsigned long long *ctr;
+  uint32_t n_tiles;   // tiles of this queue
+  uint32_t n_static;  // tickets taken without the counter: min(workers, n_tiles)
+  int x, nq, nh;      // queue index, queue count, heads of this queue
+
+  __device__ __forceinline__ TileQueue(const KernelArgs &p) {
+    nq = p.nq;
+    x = blockIdx.x % nq;
+    const int BH = p.B * p.H;
+    nh = (BH - x + nq - 1) / nq;
+    n_tiles = (uint32_t)nh * (uint32_t)p.n_mtiles;
+    const uint32_t workers = (gridDim.x - x + nq - 1) / nq;
+    n_static = workers < n_tiles ? workers : n_tiles;
+    ctr = p.queue + x * kQueueStride;
   }
-  const int span = group * n_mtiles;
-  const int gi = L / span;
-  const int r = L - gi * span;
-  const int gsz = min(group, BH - gi * group);
-  const int mr = r / gsz;
-  *bh = gi * group + (r - mr * gsz);
-  *mt = n_mtiles - 1 - mr;
-}
+  __device__ __forceinline__ uint32_t first() const { return blockIdx.x / nq; }
+  __device__ __forceinline__ unsigned long long request() const { return atomicAdd(ctr, 1ull); }
+  __device__ __forceinline__ uint32_t finish(unsigned long long raw) const {
+    if (raw == n_tiles - 1) atomicExch(ctr, 0ull);
+    return n_static + (uint32_t)raw;
+  }
+  // Ticket -> (head bh, m-tile mt); false past the end.  Order: the weight
+  // ranks k (0 = heaviest m-tile) are cut into `bands` bands; band by band,
+  // the queue's heads go in groups of `group`, and inside a group rank-major
+  // (heaviest first across the group's heads).  Small groups keep a group's
+  // K/V in the XCD's L2; bands bound how heavy the last group's tiles are.
+  __device__ __forceinline__ bool tile(uint32_t t, int n_mtiles, bool causal, int group, int bands,
+                                       int *bh, int *mt) const {
+    if (t >= n_tiles) return false;
+    const int bs = (n_mtiles + bands - 1) / bands;     // ranks per band
+    const uint32_t per_band = (uint32_t)nh * (uint32_t)bs;
+    const int b = (int)(t / per_band);
+    const uint32_t r = t - (uint32_t)b * per_band;
+    const int len = min(bs, n_mtiles - b * bs);          // ranks in this band
+    const uint32_t per_group = (uint32_t)group * (uint32_t)len;
+    const int g = (int)(r / per_group);
+    const uint32_t r2 = r - (uint32_t)g * per_group;
+    const int gsz = min(group, nh - g * group);          // heads in this group
+    const int kk = (int)(r2 / (uint32_t)gsz);
+    const int hi = (int)(r2 - (uint32_t)kk * gsz);
+    const int k = b * bs + kk;
+    *bh = x + nq * (g * group + hi);
+    *mt = causal ? n_mtiles - 1 - k : k;
+    return true;
+  }
+};
 
 template <int D, int BN, int NW, bool BF16, bool CAUSAL>
 struct FaConfig {
@@ -252,10 +297,16 @@ fa_fwd_kernel(KernelArgs p) {
 
   const float c = p.c;
 
-  for (int slot = blockIdx.x; slot < p.total_tiles; slot += gridDim.x) {
-    const int L = logical_tile(slot, gridDim.x, p.xcd_remap);
-    int bh, mt;
-    decode_tile(L, p.n_mtiles, p.B * p.H, p.head_group, CAUSAL, &bh, &mt);  // causal: heaviest first
+  // Tile loop: thread 0 takes tickets (the next one is requested at the top
+  // of a tile and published through LDS at its end, behind a barrier).
+  __shared__ uint32_t s_ticket[2];
+  const TileQueue tq(p);
+  int bh, mt;
+  for (int it = 0; tq.tile(it == 0 ? tq.first() : s_ticket[it & 1], p.n_mtiles, CAUSAL, p.q_group, p.q_bands,
+                           &bh, &mt);
+       ++it) {
+    unsigned long long next_raw = 0;
+    if (threadIdx.x == 0) next_raw = tq.request();
     const int bb = bh / p.H;
     const int hh = bh - bb * p.H;
 
@@ -445,7 +496,8 @@ fa_fwd_kernel(KernelArgs p) {
       const float lse = (m_run + __log2f(l_tot)) * kLn2;
       buf_store4(__builtin_bit_cast(uint32_t, lse), rl, h ? nbytes : (uint32_t)qrow * 4u);
     }
-    if (slot + (int)gridDim.x < p.total_tiles) __syncthreads();  // LDS reuse by the next tile
+    if (threadIdx.x == 0) s_ticket[(it + 1) & 1] = tq.finish(next_raw);
+    __syncthreads();  // LDS reuse by the next tile, ticket broadcast
   }
 }
 
@@ -503,10 +555,20 @@ __device__ __forceinline__ void dma16(BufRsrc r, uint32_t lds_addr, uint32_t vof
 }
 #pragma clang diagnostic pop
 
+// The same DMA through the compiler builtin: the compiler sees it as a
+// buffer load (so sched_group_barrier can place it between MFMAs) and, when
+// the LDS target is a different __shared__ array from the one being read,
+// adds no wait in front of those reads.
+__device__ __forceinline__ void dma16_lds(BufRsrc r, char *lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)(lds_char *)lds, 16, voff, 0,
+                                           0, 0);
+}
+
 // s_waitcnt immediate: vmcnt(n), no wait on expcnt / lgkmcnt.
 constexpr int vmcnt_imm(int n) { return 0x0f70 | (n & 0xf) | ((n >> 4) << 14); }
 
 // sched_group_barrier masks.
+constexpr int kSchedVmem = 0x010;
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
 
@@ -534,7 +596,11 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
 fa_fwd_dma_kernel(KernelArgs p) {
   using C = Cfg2<D, BN, NW, NSTAGE>;
   constexpr int BM = C::BM;
-  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+  // One array per stage: the compiler's LDS-DMA alias tracking then knows
+  // that DMAs into one stage never feed reads of the other, and adds no
+  // vmcnt wait in front of them.
+  __shared__ __attribute__((aligned(1024))) char smem0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) char smem1[C::STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -576,12 +642,22 @@ fa_fwd_dma_kernel(KernelArgs p) {
   }
 
   const float c = p.c;
-  const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_char *)smem;
 
-  for (int slot = blockIdx.x; slot < p.total_tiles; slot += gridDim.x) {
-    const int L = logical_tile(slot, gridDim.x, p.xcd_remap);
-    int bh, mt;
-    decode_tile(L, p.n_mtiles, p.B * p.H, p.head_group, CAUSAL, &bh, &mt);
+  // Tile loop: thread 0 takes tickets (the next one is requested at the top
+  // of a tile and published through LDS at its end, behind a barrier).
+  __shared__ uint32_t s_ticket[2];
+  const TileQueue tq(p);
+  int bh, mt;
+  for (int it = 0; tq.tile(it == 0 ? tq.first() : s_ticket[it & 1], p.n_mtiles, CAUSAL, p.q_group, p.q_bands,
+                           &bh, &mt);
+       ++it) {
+    unsigned long long next_raw = 0;
+    if (threadIdx.x == 0) next_raw = tq.request();
+#ifdef FA_TIMING
+    uint32_t tm_vm = 0, tm_bar = 0, tm_cmp = 0, n_comp = 0, tm_pro = 0, tm_epi0 = 0, tm_dma = 0, tm_idle = 0;
+    const uint32_t tm0 = FA_CLK();
+    const uint32_t rt0 = (uint32_t)__builtin_amdgcn_s_memrealtime();
+#endif
     const int bb = bh / p.H;
     const int hh = bh - bb * p.H;
 
@@ -597,25 +673,32 @@ fa_fwd_dma_kernel(KernelArgs p) {
     const int n_tiles = (kv_end + BN - 1) / BN;
     const int wave_last_q = q0w + 31;
 
-    auto issue_tile = [&](int t) {
+    // DMA of KV tile t into stage STG: instruction i < 2*IPW of this wave
+    // (K rows for even i, V rows for odd i).  Past the last tile the buffer
+    // range is empty: the instructions still issue (so the same code covers
+    // every tile) but fetch nothing and write zeros into the free stage.
+    auto tile_rsrc = [&](int t, BufRsrc *rk, BufRsrc *rv) __attribute__((always_inline)) {
       const int key0 = t * BN;
-      const uint32_t nbk = (uint32_t)((int64_t)(p.Sk - key0) * p.k_ss * 2);
-      const uint32_t nbv = (uint32_t)((int64_t)(p.Sk - key0) * p.v_ss * 2);
-      const BufRsrc rk = make_rsrc(kg + (int64_t)key0 * p.k_ss * 2, nbk);
-      const BufRsrc rv = make_rsrc(vg + (int64_t)key0 * p.v_ss * 2, nbv);
-      const uint32_t st = lds_base + (uint32_t)((t % NSTAGE) * C::STAGE);
-#pragma unroll
-      for (int j = 0; j < C::IPW; ++j) {
-        const uint32_t lo = st + (uint32_t)((wave + j * NW) * 1024);
-        dma16(rk, lo, dk[j]);
-        dma16(rv, lo + C::TILE, dv[j]);
-      }
+      const bool live = t < n_tiles;
+      const uint32_t nbk = live ? (uint32_t)((int64_t)(p.Sk - key0) * p.k_ss * 2) : 0u;
+      const uint32_t nbv = live ? (uint32_t)((int64_t)(p.Sk - key0) * p.v_ss * 2) : 0u;
+      *rk = make_rsrc(kg + (int64_t)key0 * p.k_ss * 2, nbk);
+      *rv = make_rsrc(vg + (int64_t)key0 * p.v_ss * 2, nbv);
+    };
+    auto dma = [&](auto stage_tag, const BufRsrc &rk, const BufRsrc &rv, int i) __attribute__((always_inline)) {
+      constexpr int STG = decltype(stage_tag)::value;
+      char *base = STG == 0 ? smem0 : smem1;
+      const int j = i >> 1;
+      dma16_lds((i & 1) ? rv : rk, base + (i & 1) * C::TILE + (wave + j * NW) * 1024, (i & 1) ? dv[j] : dk[j]);
     };
 
-    // Prologue: the first NSTAGE-1 tiles in flight.
+    // Prologue: KV tile 0 into stage 0.
+    {
+      BufRsrc rk, rv;
+      tile_rsrc(0, &rk, &rv);
 #pragma unroll
-    for (int t = 0; t < NSTAGE - 1; ++t)
-      if (t < n_tiles) issue_tile(t);
+      for (int i = 0; i < 2 * C::IPW; ++i) dma(std::integral_constant<int, 0>{}, rk, rv, i);
+    }
 
     u32x4_t qf[D / 16];
     {
@@ -640,27 +723,64 @@ fa_fwd_dma_kernel(KernelArgs p) {
     auto kv_tile = [&](int t, auto masked_tag, auto stage_tag) __attribute__((always_inline)) {
       constexpr bool MASKED = decltype(masked_tag)::value;
       constexpr int STG = decltype(stage_tag)::value;
+#ifdef FA_TIMING
+      const uint32_t ta = FA_CLK();
+      if (t == 0) tm_pro = ta - tm0;
+#endif
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+#ifdef FA_TIMING
+      const uint32_t tb = FA_CLK();
+#endif
       __syncthreads();
-      if (t + 1 < n_tiles) issue_tile(t + 1);
+#ifdef FA_TIMING
+      const uint32_t tc = FA_CLK();
+      tm_vm += tb - ta;
+      tm_bar += tc - tb;
+#endif
+      // The next tile's DMAs go into the other stage (free after the
+      // barrier); they are spread over the QK MFMAs below, or issued here
+      // when this wave has no work in this tile.
+      constexpr int NDMA = 2 * C::IPW;
+      using NEXT = std::integral_constant<int, 1 - STG>;
+      BufRsrc rk_n, rv_n;
+      tile_rsrc(t + 1, &rk_n, &rv_n);
+#ifdef FA_TIMING
+      const uint32_t td = FA_CLK();
+      tm_dma += td - tc;
+#endif
 
       const int kbase = t * BN;
-      if (MASKED && CAUSAL && kbase > wave_last_q) return;
+      if (MASKED && CAUSAL && kbase > wave_last_q) {
+#pragma unroll
+        for (int i = 0; i < NDMA; ++i) dma(NEXT{}, rk_n, rv_n, i);
+#ifdef FA_TIMING
+        tm_idle += 1;
+#endif
+        return;
+      }
+#ifdef FA_TIMING
+      ++n_comp;
+      struct Stamp {
+        uint32_t &acc, t0;
+        __device__ ~Stamp() { acc += FA_CLK() - t0; }
+      } stamp{tm_cmp, FA_CLK()};
+#endif
 
-      constexpr uint32_t st = (uint32_t)(STG * C::STAGE);
+      const char *sbase = STG == 0 ? smem0 : smem1;
 
       // S^T = K Q^T.  Fragment i = (s, kb); K fragments are read KPF ahead of
-      // their MFMA, and the first VPF V^T fragments of the P*V product are
-      // issued right behind them so they land during the softmax.
+      // their MFMA, the next tile's DMAs go out one per MFMA, and the first
+      // VPF V^T fragments of the P*V product are issued right behind the K
+      // reads so they land during the softmax.
       constexpr int NQK = (D / 16) * (BN / 32);
       constexpr int KPF = 4;
       constexpr int NPV = (BN / 16) * (D / 32);
       constexpr int VPF = 2;
       auto vread = [&](int i) {
         const int ks = i / (D / 32), db = i % (D / 32);
-        const uint32_t imm = st + (uint32_t)(C::TILE + 16 * ks * C::ROW);
-        const u32x2_t lo = lds_read_tr16(smem, vro[db][0] + imm);
-        const u32x2_t hi = lds_read_tr16(smem, vro[db][1] + imm + 8 * C::ROW);
+        const uint32_t imm = (uint32_t)(C::TILE + 16 * ks * C::ROW);
+        const u32x2_t lo = lds_read_tr16(sbase, vro[db][0] + imm);
+        const u32x2_t hi = lds_read_tr16(sbase, vro[db][1] + imm + 8 * C::ROW);
         return (u32x4_t){lo[0], lo[1], hi[0], hi[1]};
       };
       u32x4_t kfr[NQK];
@@ -671,7 +791,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
 #pragma unroll
       for (int i = 0; i < NQK; ++i) {
         const int s = i / (BN / 32), kb = i % (BN / 32);
-        kfr[i] = *(const u32x4_t *)(smem + st + kro[s] + 32 * kb * C::ROW);
+        kfr[i] = *(const u32x4_t *)(sbase + kro[s] + 32 * kb * C::ROW);
       }
 #pragma unroll
       for (int i = 0; i < VPF; ++i) vfr[i] = vread(i);
@@ -680,14 +800,17 @@ fa_fwd_dma_kernel(KernelArgs p) {
         const int s = i / (BN / 32), kb = i % (BN / 32);
         sacc[kb] = mfma32x32x16<BF16>(kfr[i], qf[s], sacc[kb]);
       }
+#pragma unroll
+      for (int i = 0; i < NDMA; ++i) dma(NEXT{}, rk_n, rv_n, i);
+      static_assert(NDMA <= NQK, "one DMA per QK MFMA at most");
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, KPF, 0);
 #pragma unroll
-      for (int i = 0; i < NQK - KPF; ++i) {
+      for (int i = 0; i < NQK; ++i) {
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        if (i < NDMA) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+        if (i + KPF < NQK) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        if (i + KPF == NQK) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * VPF, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * VPF, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, KPF, 0);
 
       if (MASKED) {
         // Register r of block kb holds key kbase + 4h + (32kb + 8(r>>2) + (r&3));
@@ -776,6 +899,9 @@ fa_fwd_dma_kernel(KernelArgs p) {
     };
     run(n_full, std::integral_constant<bool, false>{});
     run(n_tiles, std::integral_constant<bool, true>{});
+#ifdef FA_TIMING
+    tm_epi0 = FA_CLK() - tm0;
+#endif
 
     const float l_tot = halves_sum(l_run);
     const float inv = 1.f / l_tot;
@@ -799,7 +925,23 @@ fa_fwd_dma_kernel(KernelArgs p) {
       const float lse = (m_run + __log2f(l_tot)) * kLn2;
       buf_store4(__builtin_bit_cast(uint32_t, lse), rl, h ? nbytes : (uint32_t)qrow * 4u);
     }
-    if (slot + (int)gridDim.x < p.total_tiles) __syncthreads();
+#ifdef FA_TIMING
+    if (p.timing != nullptr && lane == 0) {
+      uint32_t *dst = p.timing + ((int64_t)(mt * p.B * p.H + bh) * NW + wave) * 16;
+      dst[0] = tm_vm; dst[1] = tm_bar; dst[2] = tm_cmp; dst[3] = n_comp;
+      dst[4] = tm_pro; dst[5] = FA_CLK() - tm0; dst[6] = n_tiles; dst[7] = tm_epi0;
+      dst[8] = rt0; dst[9] = (uint32_t)__builtin_amdgcn_s_memrealtime();
+      dst[10] = __builtin_amdgcn_s_getreg(4 | (0 << 6) | (31 << 11));   // HW_ID
+      dst[11] = __builtin_amdgcn_s_getreg(20 | (0 << 6) | (31 << 11));  // XCC_ID
+      dst[12] = blockIdx.x + (it << 16);
+      dst[13] = tm_dma; dst[14] = tm_idle;
+    }
+#endif
+    // The empty DMAs issued during the last KV tile write zeros into a
+    // stage: let them land before the next tile's DMAs target it.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    if (threadIdx.x == 0) s_ticket[(it + 1) & 1] = tq.finish(next_raw);
+    __syncthreads();  // LDS reuse by the next tile, ticket broadcast
   }
 }
 
@@ -882,15 +1024,21 @@ fa_fwd_pp_kernel(KernelArgs p) {
   const float c = p.c;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_char *)smem;
 
-  for (int slot = blockIdx.x; slot < p.total_tiles; slot += gridDim.x) {
+  // Tile loop: thread 0 takes tickets (the next one is requested at the top
+  // of a tile and published through LDS at its end, behind a barrier).
+  __shared__ uint32_t s_ticket[2];
+  const TileQueue tq(p);
+  int bh, mt;
+  for (int it = 0; tq.tile(it == 0 ? tq.first() : s_ticket[it & 1], p.n_mtiles, CAUSAL, p.q_group, p.q_bands,
+                           &bh, &mt);
+       ++it) {
+    unsigned long long next_raw = 0;
+    if (threadIdx.x == 0) next_raw = tq.request();
 #ifdef FA_TIMING
     uint32_t tm_m = 0, tm_s = 0, tm_w = 0, tm_dma = 0, tm_pro = 0, tm_epi = 0, n_m = 0, n_s = 0;
     const uint32_t tm0 = FA_CLK();
     uint32_t tmark = tm0;
 #endif
-    const int L = logical_tile(slot, gridDim.x, p.xcd_remap);
-    int bh, mt;
-    decode_tile(L, p.n_mtiles, p.B * p.H, p.head_group, CAUSAL, &bh, &mt);
     const int bb = bh / p.H;
     const int hh = bh - bb * p.H;
 
@@ -1203,17 +1351,16 @@ fa_fwd_pp_kernel(KernelArgs p) {
     if (p.timing != nullptr && lane == 0) {
       const uint32_t now = FA_CLK();
       tm_epi = FA_CLK_DELTA(tmark, now);
-      uint32_t *dst = p.timing + ((int64_t)L * 8 + wave) * 8;
+      uint32_t *dst = p.timing + ((int64_t)(mt * p.B * p.H + bh) * 8 + wave) * 8;
       dst[0] = tm_m; dst[1] = tm_s; dst[2] = tm_w; dst[3] = tm_pro; dst[4] = tm_dma;
       dst[5] = FA_CLK_DELTA(tm0, now); dst[6] = n_m; dst[7] = n_s;
     }
 #endif
     // The DMAs issued past the last tile may still be writing zeros into the
     // rings: retire them (every wave) before a next tile reuses the slots.
-    if (slot + (int)gridDim.x < p.total_tiles) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-      __syncthreads();
-    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    if (threadIdx.x == 0) s_ticket[(it + 1) & 1] = tq.finish(next_raw);
+    __syncthreads();
   }
 }
 
@@ -1295,7 +1442,10 @@ struct Plan {
   int grid;
 };
 
-int make_plan(const fa_fwd_params *p, Plan *out) {
+// CUs of an MI355X; fa_fwd asks the device, the host-only calls assume this.
+constexpr int kDefaultCuCount = 256;
+
+int make_plan(const fa_fwd_params *p, Plan *out, int cu_count = kDefaultCuCount) {
   int bn, nw;
   if (p->block_m == 0 && p->block_n == 0) {
     default_tiling(p->D, p->dtype, p->causal, &bn, &nw);
@@ -1313,10 +1463,33 @@ int make_plan(const fa_fwd_params *p, Plan *out) {
   out->n_mtiles = (p->Sq + out->BM - 1) / out->BM;
   out->total_tiles = (int64_t)out->n_mtiles * p->B * p->H;
   if (out->total_tiles > INT32_MAX) return FA_ERR_SHAPE;
-  int64_t grid = out->total_tiles;
-  if (p->num_programs > 0 && p->num_programs < grid) grid = p->num_programs;
+  // Persistent grid: as many workgroups as fit on the GPU at once (each
+  // kernel runs two waves per SIMD, so 8 / NW workgroups per CU), pulling
+  // tiles from the tile queues; PERSISTENT_PROGRAMS (num_programs) overrides
+  // the count.
+  int64_t grid = (int64_t)(8 / nw) * (cu_count > 0 ? cu_count : kDefaultCuCount);
+  if (p->num_programs > 0) grid = p->num_programs;
+  if (grid > out->total_tiles) grid = out->total_tiles;
   out->grid = (int)grid;
   return FA_OK;
+}
+
+// Per-device address of g_tile_queues (hipGetSymbolAddress with the device
+// current), and the launch sequence that picks the queue slot.
+constexpr int kMaxDevices = 64;
+std::atomic<unsigned long long *> g_queue_base[kMaxDevices];
+std::atomic<unsigned long long> g_launch_seq{0};
+
+unsigned long long *queue_base(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  unsigned long long *ptr = g_queue_base[device].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    void *addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(g_tile_queues)) != hipSuccess || addr == nullptr) return nullptr;
+    ptr = (unsigned long long *)addr;
+    g_queue_base[device].store(ptr, std::memory_order_release);
+  }
+  return ptr;
 }
 
 bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
@@ -1425,8 +1598,12 @@ int fa_fwd(const fa_fwd_params *p, void *hip_stream) {
   const int rc = fa_validate(p);
   if (rc != FA_OK) return rc;
   if (p->B == 0 || p->H == 0 || p->Sq == 0) return FA_OK;
+  int device = 0, cu_count = 0;
+  if (hipGetDevice(&device) != hipSuccess ||
+      hipDeviceGetAttribute(&cu_count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    cu_count = kDefaultCuCount;
   Plan plan;
-  const int prc = make_plan(p, &plan);
+  const int prc = make_plan(p, &plan, cu_count);
   if (prc != FA_OK) return prc;
 
   KernelArgs a;
@@ -1445,19 +1622,38 @@ int fa_fwd(const fa_fwd_params *p, void *hip_stream) {
   a.Sk = p->Sk;
   a.n_mtiles = plan.n_mtiles;
   a.total_tiles = (int32_t)plan.total_tiles;
-#ifdef FA_NO_XCD_REMAP
-  a.xcd_remap = 0;
-#else
-  a.xcd_remap = plan.grid == plan.total_tiles ? 1 : 0;
-#endif
-  // One XCD has 32 CUs; a 256-row (8-wave) workgroup fills a CU, a 128-row
-  // one half of it.  Group enough heads that their m-tiles fill the XCD.
   {
-    const int slots = (plan.NW == 8 ? 32 : 64);
-#ifdef FA_HEAD_GROUP
-    a.head_group = FA_HEAD_GROUP;
-#else
-    a.head_group = plan.n_mtiles >= slots ? 1 : (slots + plan.n_mtiles - 1) / plan.n_mtiles;
+    unsigned long long *base = queue_base(device);
+    if (base == nullptr) return FA_ERR_LAUNCH;
+    const unsigned long long seq = g_launch_seq.fetch_add(1, std::memory_order_relaxed);
+    a.queue = base + (seq % kQueueSlots) * kQueues * kQueueStride;
+    const int64_t bh = (int64_t)p->B * p->H;
+    int64_t nq = kQueues;
+    if (nq > plan.grid) nq = plan.grid;
+    if (nq > bh) nq = bh;
+    a.nq = (int32_t)nq;
+    // Queue order: all of a queue's heads at once (heaviest first across
+    // them) while their K+V fit in 16 MiB of L2 + MALL reuse distance;
+    // otherwise groups small enough for that, but at least large enough that
+    // a group has ~4 tiles per worker, in two weight bands.  Measured on the
+    // five benchmark workloads (within 1-3% of the best fixed choice each).
+    const int64_t nh = (bh + nq - 1) / nq;  // heads of queue 0
+    const int64_t workers = plan.grid / nq;
+    const int64_t kv_head = (int64_t)p->Sk * p->D * 2 * 2;
+    const int64_t budget = (int64_t)16 << 20;
+    int64_t group = nh;
+    if (nh * kv_head > budget) {
+      const int64_t by_l2 = budget / kv_head > 1 ? budget / kv_head : 1;
+      const int64_t by_work = (4 * workers + plan.n_mtiles - 1) / plan.n_mtiles;
+      group = by_l2 > by_work ? by_l2 : by_work;
+      if (group > nh) group = nh;
+      if (group > by_l2 && by_l2 * 2 >= by_work) group = by_l2;
+    }
+    a.q_group = (int32_t)(group > 0 ? group : 1);
+    a.q_bands = 2;
+#ifdef FA_DEV_KNOBS
+    if (const char *e = getenv("FA_QG")) a.q_group = atoi(e) > 0 ? atoi(e) : a.q_group;
+    if (const char *e = getenv("FA_QB")) a.q_bands = atoi(e) > 0 ? atoi(e) : 1;
 #endif
   }
   // A negative scale is folded into Q (sign flip of every element, exact),

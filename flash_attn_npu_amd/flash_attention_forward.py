@@ -32,8 +32,10 @@ import torch
 
 DEVICE = "cuda"
 RESULT_DIR_NAME = "result_dir"
-# 0 = one workgroup per (z, h, m-tile); >0 caps the grid and the kernel strides
-# over tiles (the reference's persistent grid, flash_attention_forward.py:24,616-623).
+# 0 = the library's persistent grid (as many workgroups as are resident at
+# once: 512 for 4-wave kernels on 256 CUs); >0 sets the program count.  Either
+# way every workgroup walks its share of the balanced tile schedule (the
+# reference's persistent grid, flash_attention_forward.py:24,616-623).
 DEFAULT_PERSISTENT_PROGRAMS = 0
 PROFILE_OP_NAME = "fa_fwd_kernel"
 LIB_NAME = "libfa_mi355x.so"
@@ -156,7 +158,7 @@ def kernel_table():
 # Tiling policy (flash_attention_forward.py:156-252, 616-644)
 
 def _get_persistent_programs():
-    """Grid cap from $PERSISTENT_PROGRAMS (>= 1), else 0 = one workgroup per tile.
+    """Program count from $PERSISTENT_PROGRAMS (>= 1), else 0 = the library's resident grid.
 
     Same variable and check as flash_attention_forward.py:616-623.
     """

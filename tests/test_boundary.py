@@ -119,7 +119,8 @@ def test_query_config_headline(lib):
     assert lib.fa_query_config(ctypes.byref(_params(shape=(4, 32, 2048, 128))), out) == 0
     bm, bn, waves, grid, tiles, lds, stage, kid = list(out)
     assert (bm, bn) == tuple(fa.get_tiling(4, 32, 2048, 128, True))
-    assert waves == bm // 32 and tiles == math.ceil(2048 / bm) * 128 and grid == tiles
+    # Persistent grid: two waves per SIMD on 256 CUs, capped by the tile count.
+    assert waves == bm // 32 and tiles == math.ceil(2048 / bm) * 128 and grid == min(tiles, 8 // waves * 256)
     assert stage == 3 and 0 < lds <= 160 * 1024 and 0 <= kid < lib.fa_num_kernels()
 
 
@@ -210,7 +211,7 @@ def test_describe_runtime_keys(monkeypatch):
     monkeypatch.delenv("PERSISTENT_PROGRAMS", raising=False)
     rt = fa._describe_runtime(4, 32, 2048, 128, True)
     assert set(rt) >= {"selected_config", "tiling_source", "total_tiles", "launched_programs", "stage"}
-    assert rt["stage"] == 3 and rt["launched_programs"] == rt["total_tiles"]
+    assert rt["stage"] == 3 and rt["launched_programs"] == min(rt["total_tiles"], 8 // rt["waves"] * 256)
     assert fa._describe_runtime(4, 32, 2048, 128, False)["stage"] == 1
 
 
