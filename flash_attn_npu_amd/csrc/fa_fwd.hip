@@ -515,18 +515,30 @@ fa_fwd_kernel(KernelArgs p) {
 //    ds_read_b128 phase (16 consecutive keys, one logical chunk) hit 16
 //    distinct bank slots; and for the 4 consecutive rows of a transpose read
 //    the high two bits (r & 3) separate their 4-chunk blocks.
+//  * D = 256 (512-byte rows): the D = 128 swizzle; only a chunk's position
+//    modulo 16 picks its banks, and rows 512 bytes apart align like rows 256
+//    bytes apart.
 //  * D = 64 (128-byte rows, two per bank row): swz = 4 ((r >> 1) & 1) +
 //    ((r >> 2) & 3), a permutation over r >> 1 within each half of the bank
 //    row, with rows r and r + 2 of a transpose read in different 4-chunk
 //    blocks.
+//  * D = 32 (64-byte rows, four per bank row): swz = (r >> 2) & 3 separates
+//    rows r, r+4, r+8, r+12 of a ds_read_b128 phase.
+//  * D = 16 (32-byte rows, eight per bank row): swz = (r >> 3) & 1 separates
+//    rows r and r+8.
 // Every DMA instruction still writes 1 KB contiguously and reads whole rows
 // from HBM.
 template <int D>
 __device__ __forceinline__ int swz(int r) {
-  if constexpr (D == 128) {
+  if constexpr (D == 128 || D == 256) {
     return ((r & 3) << 2) | ((r >> 2) & 3);
-  } else {
+  } else if constexpr (D == 64) {
     return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  } else if constexpr (D == 32) {
+    return (r >> 2) & 3;
+  } else {
+    static_assert(D == 16, "head dim");
+    return (r >> 3) & 1;
   }
 }
 
@@ -572,7 +584,7 @@ constexpr int kSchedVmem = 0x010;
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
 
-template <int D, int BN, int NW, int NSTAGE>
+template <int D, int BN, int NW, int NSTAGE, int OCC>
 struct Cfg2 {
   static constexpr int BM = 32 * NW;
   static constexpr int NT = 64 * NW;
@@ -584,17 +596,21 @@ struct Cfg2 {
   static constexpr int IPW = IPT / NW;        // ... per wave
   static constexpr int STAGE = 2 * TILE;
   static constexpr int LDS_BYTES = NSTAGE * STAGE;
-  static_assert(CPR >= 8, "the swizzle needs at least 8 chunks per row");
+  // O^T blocks of 32 head dims; D = 16 uses one block whose upper 16 rows
+  // come out zero (the V^T operand rows past D are zeroed).
+  static constexpr int DB = D >= 32 ? D / 32 : 1;
+  static_assert(D == 16 || D == 32 || D == 64 || D == 128 || D == 256, "head dim");
   static_assert(IPT % NW == 0 && IPW >= 1, "DMA instructions must split evenly over waves");
-  static_assert(BN % 32 == 0 && D % 32 == 0, "tile shape");
+  static_assert(BN % 32 == 0, "tile shape");
   static_assert(NSTAGE == 2, "double-buffered: one tile computes while the next lands");
-  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one gfx950 CU");
+  static_assert(OCC == 1 || OCC == 2, "workgroups per CU");
+  static_assert(LDS_BYTES * OCC <= 160 * 1024, "LDS budget of one gfx950 CU");
 };
 
-template <int D, int BN, int NW, int NSTAGE, bool BF16, bool CAUSAL>
-__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int D, int BN, int NW, int NSTAGE, int OCC, bool BF16, bool CAUSAL>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC * NW / 4, OCC * NW / 4)))
 fa_fwd_dma_kernel(KernelArgs p) {
-  using C = Cfg2<D, BN, NW, NSTAGE>;
+  using C = Cfg2<D, BN, NW, NSTAGE, OCC>;
   constexpr int BM = C::BM;
   // One array per stage: the compiler's LDS-DMA alias tracking then knows
   // that DMAs into one stage never feed reads of the other, and adds no
@@ -628,15 +644,17 @@ fa_fwd_dma_kernel(KernelArgs p) {
   // 4j + c points at key row 16ks + 8e + 4h + j, dims 32db + 16(g&1) + 4c
   // (logical chunk 4db + 2(g&1) + c/2).  swz of that row depends only on
   // (e, h, j), so one lane offset per (db, e) covers every k-step ks.
-  uint32_t vro[D / 32][2];
+  // D = 16: lanes of the upper 16 dims read dims 0..15 again (in range) and
+  // their fragments are zeroed before use.
+  uint32_t vro[C::DB][2];
   {
     const int g = lane >> 4, sg = lane & 15, jj = sg >> 2, cc = sg & 3;
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db)
+    for (int db = 0; db < C::DB; ++db)
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int row = 8 * e + 4 * h + jj;
-        const int lc = 4 * db + 2 * (g & 1) + (cc >> 1);
+        const int lc = 4 * db + (D >= 32 ? 2 * (g & 1) : 0) + (cc >> 1);
         vro[db][e] = (uint32_t)((4 * h + jj) * C::ROW + ((lc ^ swz<D>(row)) * 16) + (cc & 1) * 8);
       }
   }
@@ -708,9 +726,9 @@ fa_fwd_dma_kernel(KernelArgs p) {
       for (int s = 0; s < D / 16; ++s) qf[s] = buf_load16(rq, qo + 32 * s) ^ p.q_sign;
     }
 
-    f32x16_t oacc[D / 32];
+    f32x16_t oacc[C::DB];
 #pragma unroll
-    for (int db = 0; db < D / 32; ++db) oacc[db] = (f32x16_t){};
+    for (int db = 0; db < C::DB; ++db) oacc[db] = (f32x16_t){};
     float m_run = -INFINITY;
     float l_run = 0.f;
 
@@ -774,35 +792,44 @@ fa_fwd_dma_kernel(KernelArgs p) {
       // reads so they land during the softmax.
       constexpr int NQK = (D / 16) * (BN / 32);
       constexpr int KPF = 4;
-      constexpr int NPV = (BN / 16) * (D / 32);
+      constexpr int NPV = (BN / 16) * C::DB;
       constexpr int VPF = 2;
       auto vread = [&](int i) {
-        const int ks = i / (D / 32), db = i % (D / 32);
+        const int ks = i / C::DB, db = i % C::DB;
         const uint32_t imm = (uint32_t)(C::TILE + 16 * ks * C::ROW);
         const u32x2_t lo = lds_read_tr16(sbase, vro[db][0] + imm);
         const u32x2_t hi = lds_read_tr16(sbase, vro[db][1] + imm + 8 * C::ROW);
-        return (u32x4_t){lo[0], lo[1], hi[0], hi[1]};
+        u32x4_t f = {lo[0], lo[1], hi[0], hi[1]};
+        if constexpr (D < 32) {
+          if (lane & 16) f = (u32x4_t){0u, 0u, 0u, 0u};
+        }
+        return f;
       };
       u32x4_t kfr[NQK];
       u32x4_t vfr[NPV];
       f32x16_t sacc[BN / 32];
 #pragma unroll
       for (int kb = 0; kb < BN / 32; ++kb) sacc[kb] = (f32x16_t){};
-#pragma unroll
-      for (int i = 0; i < NQK; ++i) {
+      // Written in issue order (read i + KPF, MFMA i, DMA i), which also
+      // bounds the fragments' live ranges if the schedule below is relaxed.
+      auto kread = [&](int i) {
         const int s = i / (BN / 32), kb = i % (BN / 32);
-        kfr[i] = *(const u32x4_t *)(sbase + kro[s] + 32 * kb * C::ROW);
-      }
+        return *(const u32x4_t *)(sbase + kro[s] + 32 * kb * C::ROW);
+      };
 #pragma unroll
-      for (int i = 0; i < VPF; ++i) vfr[i] = vread(i);
+      for (int i = 0; i < KPF && i < NQK; ++i) kfr[i] = kread(i);
+      static_assert(NDMA <= NQK, "one DMA per QK MFMA at most");
 #pragma unroll
       for (int i = 0; i < NQK; ++i) {
+        if (i + KPF < NQK) kfr[i + KPF] = kread(i + KPF);
+        if (i + KPF == NQK) {
+#pragma unroll
+          for (int j = 0; j < VPF; ++j) vfr[j] = vread(j);
+        }
         const int s = i / (BN / 32), kb = i % (BN / 32);
         sacc[kb] = mfma32x32x16<BF16>(kfr[i], qf[s], sacc[kb]);
+        if (i < NDMA) dma(NEXT{}, rk_n, rv_n, i);
       }
-#pragma unroll
-      for (int i = 0; i < NDMA; ++i) dma(NEXT{}, rk_n, rv_n, i);
-      static_assert(NDMA <= NQK, "one DMA per QK MFMA at most");
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, KPF, 0);
 #pragma unroll
       for (int i = 0; i < NQK; ++i) {
@@ -839,7 +866,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
         const float alpha = upd ? fast_exp2(m_run - m_new) : 1.f;
         l_run *= alpha;
 #pragma unroll
-        for (int db = 0; db < D / 32; ++db) oacc[db] *= alpha;
+        for (int db = 0; db < C::DB; ++db) oacc[db] *= alpha;
       }
       m_run = m_new;
       const float mb = (m_new == -INFINITY) ? 0.f : m_new;
@@ -867,10 +894,9 @@ fa_fwd_dma_kernel(KernelArgs p) {
       // O^T += V^T P^T; the A operand is two transpose reads (keys +0..3 and
       // +8..11 of the k-step), VPF fragments ahead of their MFMA.
 #pragma unroll
-      for (int i = VPF; i < NPV; ++i) vfr[i] = vread(i);
-#pragma unroll
       for (int i = 0; i < NPV; ++i) {
-        const int ks = i / (D / 32), db = i % (D / 32);
+        if (i + VPF < NPV) vfr[i + VPF] = vread(i + VPF);
+        const int ks = i / C::DB, db = i % C::DB;
         oacc[db] = mfma32x32x16<BF16>(vfr[i], pf[ks], oacc[db]);
       }
 #pragma unroll
@@ -910,9 +936,9 @@ fa_fwd_dma_kernel(KernelArgs p) {
       const BufRsrc ro = make_rsrc(og, (uint32_t)((int64_t)p.Sq * p.o_ss * 2));
       const uint32_t oo = (uint32_t)(qrow * p.o_ss * 2 + 8 * h);
 #pragma unroll
-      for (int db = 0; db < D / 32; ++db)
+      for (int db = 0; db < C::DB; ++db)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < (D >= 32 ? 4 : 2); ++j) {  // rows 8j + 4h + 0..3 of the block
           u32x2_t x;
           x[0] = pack2<BF16>(oacc[db][4 * j + 0] * inv, oacc[db][4 * j + 1] * inv);
           x[1] = pack2<BF16>(oacc[db][4 * j + 2] * inv, oacc[db][4 * j + 3] * inv);
@@ -1370,59 +1396,62 @@ typedef void (*KernelFn)(KernelArgs);
 
 struct KernelEntry {
   int32_t D, dtype, causal, BN, NW;
-  int32_t stages;  // LDS stages of the DMA kernel; 0 = register-staged kernel
+  int32_t stages;     // LDS stages of the DMA kernel; 0 = register-staged kernel
   int32_t lds_bytes;
+  int32_t wg_per_cu;  // resident workgroups per CU (registers and LDS)
   KernelFn fn;
 };
 
 template <int D, int BN, int NW, bool BF16, bool CAUSAL>
 constexpr KernelEntry entry() {
   return KernelEntry{D, BF16 ? 1 : 0, CAUSAL ? 1 : 0, BN, NW, 0,
-                     FaConfig<D, BN, NW, BF16, CAUSAL>::LDS_BYTES,
+                     FaConfig<D, BN, NW, BF16, CAUSAL>::LDS_BYTES, 8 / NW,
                      fa_fwd_kernel<D, BN, NW, BF16, CAUSAL>};
 }
 
-template <int D, int BN, int NW, int NSTAGE, bool BF16, bool CAUSAL>
+template <int D, int BN, int NW, int NSTAGE, int OCC, bool BF16, bool CAUSAL>
 constexpr KernelEntry entry_dma() {
   return KernelEntry{D, BF16 ? 1 : 0, CAUSAL ? 1 : 0, BN, NW, NSTAGE,
-                     Cfg2<D, BN, NW, NSTAGE>::LDS_BYTES,
-                     fa_fwd_dma_kernel<D, BN, NW, NSTAGE, BF16, CAUSAL>};
+                     Cfg2<D, BN, NW, NSTAGE, OCC>::LDS_BYTES, OCC,
+                     fa_fwd_dma_kernel<D, BN, NW, NSTAGE, OCC, BF16, CAUSAL>};
 }
 
 #define FA_ENTRIES_DT_C(D, BN, NW)                                                   \
   entry<D, BN, NW, false, false>(), entry<D, BN, NW, false, true>(),                 \
       entry<D, BN, NW, true, false>(), entry<D, BN, NW, true, true>()
-#define FA_PP_ENTRIES(D, BN, NR)                                                     \
-  KernelEntry{D, 0, 0, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, fa_fwd_pp_kernel<D, BN, NR, false, false>}, \
-  KernelEntry{D, 0, 1, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, fa_fwd_pp_kernel<D, BN, NR, false, true>},  \
-  KernelEntry{D, 1, 0, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, fa_fwd_pp_kernel<D, BN, NR, true, false>},  \
-  KernelEntry{D, 1, 1, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, fa_fwd_pp_kernel<D, BN, NR, true, true>}
-#define FA_DMA_ENTRIES(D, BN, NW, ST)                                                \
-  entry_dma<D, BN, NW, ST, false, false>(), entry_dma<D, BN, NW, ST, false, true>(), \
-      entry_dma<D, BN, NW, ST, true, false>(), entry_dma<D, BN, NW, ST, true, true>()
+#define FA_PP_ENTRIES(D, BN, NR)                                                                     \
+  KernelEntry{D, 0, 0, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, fa_fwd_pp_kernel<D, BN, NR, false, false>}, \
+  KernelEntry{D, 0, 1, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, fa_fwd_pp_kernel<D, BN, NR, false, true>},  \
+  KernelEntry{D, 1, 0, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, fa_fwd_pp_kernel<D, BN, NR, true, false>},  \
+  KernelEntry{D, 1, 1, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, fa_fwd_pp_kernel<D, BN, NR, true, true>}
+#define FA_DMA_ENTRIES(D, BN, NW, ST, OCC)                                                     \
+  entry_dma<D, BN, NW, ST, OCC, false, false>(), entry_dma<D, BN, NW, ST, OCC, false, true>(), \
+      entry_dma<D, BN, NW, ST, OCC, true, false>(), entry_dma<D, BN, NW, ST, OCC, true, true>()
 
+// The first entry matching (D, dtype, causal, BLOCK_N, waves) serves a launch.
 const KernelEntry kKernels[] = {
-#ifdef FA_PREFER_REGISTER_STAGED
-    FA_ENTRIES_DT_C(64, 64, 4),
-    FA_ENTRIES_DT_C(128, 64, 4),
-#endif
-    FA_DMA_ENTRIES(128, 64, 4, 2),
+    FA_DMA_ENTRIES(128, 64, 4, 2, 2),
     FA_PP_ENTRIES(128, 64, 4),
-    FA_DMA_ENTRIES(64, 64, 4, 2),
+    FA_DMA_ENTRIES(64, 64, 4, 2, 2),
     FA_PP_ENTRIES(64, 64, 4),
+    // D = 256: 512 registers per wave (O^T alone is 128), so one workgroup
+    // per CU; 32-key tiles keep S, P and the operand fragments small.
+    FA_DMA_ENTRIES(256, 32, 4, 2, 1),
+    FA_DMA_ENTRIES(32, 64, 4, 2, 2),
+    // D = 16: a 64-key tile is only two DMA instructions; 128 keys give each wave one.
+    FA_DMA_ENTRIES(16, 128, 4, 2, 2),
     FA_ENTRIES_DT_C(64, 64, 4),
     FA_ENTRIES_DT_C(128, 64, 4),
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
-bool is_supported_head_dim(int d) { return d == 64 || d == 128; }
+bool is_supported_head_dim(int d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
 
 // Default (BLOCK_N, waves) per head dim; BLOCK_M = 32 * waves.
 void default_tiling(int D, int dtype, int causal, int *bn, int *nw) {
   (void)dtype;
   (void)causal;
-  (void)D;
-  *bn = 64;
+  *bn = D == 16 ? 128 : (D == 256 ? 32 : 64);
   *nw = 4;
 }
 
@@ -1467,7 +1496,7 @@ int make_plan(const fa_fwd_params *p, Plan *out, int cu_count = kDefaultCuCount)
   // kernel runs two waves per SIMD, so 8 / NW workgroups per CU), pulling
   // tiles from the tile queues; PERSISTENT_PROGRAMS (num_programs) overrides
   // the count.
-  int64_t grid = (int64_t)(8 / nw) * (cu_count > 0 ? cu_count : kDefaultCuCount);
+  int64_t grid = (int64_t)kKernels[kid].wg_per_cu * (cu_count > 0 ? cu_count : kDefaultCuCount);
   if (p->num_programs > 0) grid = p->num_programs;
   if (grid > out->total_tiles) grid = out->total_tiles;
   out->grid = (int)grid;

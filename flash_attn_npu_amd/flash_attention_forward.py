@@ -39,7 +39,7 @@ RESULT_DIR_NAME = "result_dir"
 DEFAULT_PERSISTENT_PROGRAMS = 0
 PROFILE_OP_NAME = "fa_fwd_kernel"
 LIB_NAME = "libfa_mi355x.so"
-SUPPORTED_HEAD_DIMS = (64, 128)
+SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
 # The reference accepts these head dims (flash_attention_forward.py:1121-1122).
 REFERENCE_HEAD_DIMS = (16, 32, 64, 128, 256)
 

@@ -78,6 +78,8 @@ def test_validate_accepts_good_params(lib):
     assert lib.fa_validate(ctypes.byref(_params())) == 0
     assert lib.fa_validate(ctypes.byref(_params(lse=None))) == 0
     assert lib.fa_validate(ctypes.byref(_params(shape=(0, 4, 128, 128)))) == 0  # empty is fine
+    for d in (16, 32, 64, 128, 256):  # every head dim of flash_attention_forward.py:1121
+        assert lib.fa_validate(ctypes.byref(_params(shape=(1, 2, 128, d)))) == 0, d
 
 
 @pytest.mark.parametrize("mutate,code", [
@@ -85,6 +87,7 @@ def test_validate_accepts_good_params(lib):
     (lambda p: setattr(p, "Sq", -1), -2),
     (lambda p: setattr(p, "Sk", 0), -2),
     (lambda p: setattr(p, "D", 96), -3),
+    (lambda p: setattr(p, "D", 48), -3),
     (lambda p: setattr(p, "dtype", 7), -4),
     (lambda p: p.k_stride.__setitem__(3, 2), -5),
     (lambda p: p.v_stride.__setitem__(2, 12), -5),
@@ -170,7 +173,7 @@ def test_module_loads_by_path():
     (((2, 3, 4), (2, 3, 4), (2, 3, 4)), "4D"),
     (((1, 2, 8, 64), (1, 2, 9, 64), (1, 2, 8, 64)), "same shape"),
     (((1, 2, 8, 48), (1, 2, 8, 48), (1, 2, 8, 48)), "HEAD_DIM must be one of"),
-    (((1, 2, 8, 256), (1, 2, 8, 256), (1, 2, 8, 256)), "not supported by this build"),
+    (((1, 2, 8, 96), (1, 2, 8, 96), (1, 2, 8, 96)), "HEAD_DIM must be one of"),
 ])
 def test_validate_inputs_like_reference(shapes, msg):
     q, k, v = (torch.zeros(s, dtype=torch.float16) for s in shapes)

@@ -93,7 +93,7 @@ RAGGED = [1, 2, 17, 31, 32, 33, 63, 64, 65, 100, 127, 128, 129, 191, 255, 257, 3
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 def test_ragged_lengths_vs_oracle(fa, dtype, d, causal):
     g = torch.Generator().manual_seed(1234 + d)
@@ -108,6 +108,26 @@ def test_ragged_lengths_vs_oracle(fa, dtype, d, causal):
         d_l = np.abs(lse.cpu().numpy() - l_ref).max()
         assert d_o <= O_TOL[dtype], (s, d_o)
         assert d_l <= LSE_TOL, (s, d_l)
+
+
+@pytest.mark.parametrize("shape", [(2, 8, 1024, 256, True), (1, 8, 2048, 256, False), (4, 16, 777, 32, True),
+                                   (3, 16, 1500, 16, False), (2, 4, 4096, 16, True)],
+                         ids=lambda s: "x".join(map(str, s[:4])) + ("c" if s[4] else "f"))
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_other_head_dims_at_scale(fa, shape, dtype):
+    """D = 16, 32, 256 (flash_attention_forward.py:1121) at evaluator-like sizes, all heads vs float64.
+
+    The first two shapes are the evaluator's D = 256 performance cases
+    (evaluate_attention.py:38, :40) with a smaller batch.
+    """
+    z, h, s, d, causal = shape
+    _say(f"[head dims] {shape} {DT_NAME[dtype]}")
+    g = torch.Generator().manual_seed(77 + d)
+    q, k, v = ((torch.randn((z, h, s, d), generator=g) * 0.5).to(dtype).cuda() for _ in range(3))
+    out, lse = fa.attention(q, k, v, causal, 0.5, return_lse=True)
+    o64, l64 = attention_fp64(q, k, v, causal, 0.5)
+    assert (out.float() - o64.to(dtype).float()).abs().max().item() <= O_TOL[dtype]
+    assert (lse.double() - l64).abs().max().item() <= LSE_TOL
 
 
 def test_strided_inputs_read_in_place(fa):
