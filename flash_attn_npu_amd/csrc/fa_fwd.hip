@@ -1432,8 +1432,10 @@ constexpr KernelEntry entry_dma() {
 const KernelEntry kKernels[] = {
     FA_DMA_ENTRIES(128, 64, 4, 2, 2),
     FA_PP_ENTRIES(128, 64, 4),
+    FA_DMA_ENTRIES(128, 32, 4, 2, 2),
     FA_DMA_ENTRIES(64, 64, 4, 2, 2),
     FA_PP_ENTRIES(64, 64, 4),
+    FA_DMA_ENTRIES(64, 32, 4, 2, 2),
     // D = 256: 512 registers per wave (O^T alone is 128), so one workgroup
     // per CU; 32-key tiles keep S, P and the operand fragments small.
     FA_DMA_ENTRIES(256, 32, 4, 2, 1),

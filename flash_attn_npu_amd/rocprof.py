@@ -171,7 +171,11 @@ def run_passes(out: Path, target: list[str], plan=None, timeout=120) -> dict:
     plan = METRIC_PLAN if plan is None else plan
     out = Path(out).resolve()
     out.mkdir(parents=True, exist_ok=True)
-    env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
+    # The passes run from /tmp (rocprofv3 writes scratch files there); keep
+    # this repository importable for a `python -m flash_attn_npu_amd...` target.
+    repo = str(Path(__file__).resolve().parent.parent)
+    env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"),
+               PYTHONPATH=os.pathsep.join(p for p in (repo, os.environ.get("PYTHONPATH", "")) if p))
     summary = {}
     for name, counters in plan.items():
         pdir = out / name
