@@ -45,8 +45,14 @@ REFERENCE_HEAD_DIMS = (16, 32, 64, 128, 256)
 
 # BEGIN AUTO-TUNED DEFAULT TILING PRESETS
 # (Z, H, N_CTX, HEAD_DIM, causal) -> (BLOCK_M, BLOCK_N), rewritten by
-# tune_flash_attention_forward.py from gfx950 sweeps.
+# python -m flash_attn_npu_amd.tune from gfx950 sweeps.
 DEFAULT_TILING_PRESETS = {
+    (128, 8, 1024, 128, True): (128, 32),
+    (128, 8, 1024, 256, True): (128, 32),
+    (128, 8, 2048, 128, True): (128, 32),
+    (128, 8, 2048, 256, False): (128, 32),
+    (128, 8, 4096, 128, False): (128, 32),
+    (128, 8, 8192, 64, False): (128, 64),
 }
 # END AUTO-TUNED DEFAULT TILING PRESETS
 
