@@ -88,6 +88,14 @@ struct KernelArgs {
   int32_t nq;                 // tile queues: min(8, grid, B*H)
   int32_t q_group;            // heads per group in a queue's order (>= 1)
   int32_t q_bands;            // weight bands in a queue's order (>= 1)
+  // Split-KV (DMA kernel only): kv_splits > 1 cuts every m-tile's KV range
+  // into runs of split_tiles tiles; each run writes a partial O (fp32,
+  // normalised by its own row sum) and its natural-log LSE, and
+  // fa_merge_kernel combines them.  kv_splits == 1: O and LSE directly.
+  int32_t kv_splits;
+  int32_t split_tiles;
+  float *part_o;              // [kv_splits][B*H][Sq][D]
+  float *part_lse;            // [kv_splits][B*H][Sq]
   uint32_t q_sign;      // 0x80008000 when sm_scale < 0 (Q is negated in registers)
   float c;              // |sm_scale| * log2(e), > 0
   uint32_t *timing;     // per-wave phase cycle counts (FA_TIMING builds only), else null
@@ -150,6 +158,9 @@ __device__ __forceinline__ u32x4_t buf_load16(BufRsrc r, uint32_t voff) {
 __device__ __forceinline__ void buf_store8(u32x2_t v, BufRsrc r, uint32_t voff) {
   __builtin_amdgcn_raw_buffer_store_b64(v, r, voff, 0, 0);
 }
+__device__ __forceinline__ void buf_store16(u32x4_t v, BufRsrc r, uint32_t voff) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, 0, 0);
+}
 __device__ __forceinline__ void buf_store4(uint32_t v, BufRsrc r, uint32_t voff) {
   __builtin_amdgcn_raw_buffer_store_b32(v, r, voff, 0, 0);
 }
@@ -205,7 +216,7 @@ struct TileQueue {
     x = blockIdx.x % nq;
     const int BH = p.B * p.H;
     nh = (BH - x + nq - 1) / nq;
-    n_tiles = (uint32_t)nh * (uint32_t)p.n_mtiles;
+    n_tiles = (uint32_t)nh * (uint32_t)p.n_mtiles * (uint32_t)p.kv_splits;
     const uint32_t workers = (gridDim.x - x + nq - 1) / nq;
     n_static = workers < n_tiles ? workers : n_tiles;
     ctr = p.queue + x * kQueueStride;
@@ -216,14 +227,19 @@ struct TileQueue {
     if (raw == n_tiles - 1) atomicExch(ctr, 0ull);
     return n_static + (uint32_t)raw;
   }
-  // Ticket -> (head bh, m-tile mt); false past the end.  Order: the weight
-  // ranks k (0 = heaviest m-tile) are cut into `bands` bands; band by band,
-  // the queue's heads go in groups of `group`, and inside a group rank-major
-  // (heaviest first across the group's heads).  Small groups keep a group's
-  // K/V in the XCD's L2; bands bound how heavy the last group's tiles are.
+  // Ticket -> (head bh, m-tile mt, KV split); false past the end.  Order:
+  // KV splits one after the other (split 0 holds the most work); inside a
+  // split, the weight ranks k (0 = heaviest m-tile) are cut into `bands`
+  // bands; band by band, the queue's heads go in groups of `group`, and
+  // inside a group rank-major (heaviest first across the group's heads).
+  // Small groups keep a group's K/V in the XCD's L2; bands bound how heavy
+  // the last group's tiles are.
   __device__ __forceinline__ bool tile(uint32_t t, int n_mtiles, bool causal, int group, int bands,
-                                       int *bh, int *mt) const {
+                                       int *bh, int *mt, int *split) const {
     if (t >= n_tiles) return false;
+    const uint32_t per_split = (uint32_t)nh * (uint32_t)n_mtiles;
+    *split = (int)(t / per_split);
+    t -= (uint32_t)*split * per_split;
     const int bs = (n_mtiles + bands - 1) / bands;     // ranks per band
     const uint32_t per_band = (uint32_t)nh * (uint32_t)bs;
     const int b = (int)(t / per_band);
@@ -301,9 +317,9 @@ fa_fwd_kernel(KernelArgs p) {
   // of a tile and published through LDS at its end, behind a barrier).
   __shared__ uint32_t s_ticket[2];
   const TileQueue tq(p);
-  int bh, mt;
+  int bh, mt, split;
   for (int it = 0; tq.tile(it == 0 ? tq.first() : s_ticket[it & 1], p.n_mtiles, CAUSAL, p.q_group, p.q_bands,
-                           &bh, &mt);
+                           &bh, &mt, &split);
        ++it) {
     unsigned long long next_raw = 0;
     if (threadIdx.x == 0) next_raw = tq.request();
@@ -665,9 +681,9 @@ fa_fwd_dma_kernel(KernelArgs p) {
   // of a tile and published through LDS at its end, behind a barrier).
   __shared__ uint32_t s_ticket[2];
   const TileQueue tq(p);
-  int bh, mt;
+  int bh, mt, split;
   for (int it = 0; tq.tile(it == 0 ? tq.first() : s_ticket[it & 1], p.n_mtiles, CAUSAL, p.q_group, p.q_bands,
-                           &bh, &mt);
+                           &bh, &mt, &split);
        ++it) {
     unsigned long long next_raw = 0;
     if (threadIdx.x == 0) next_raw = tq.request();
@@ -688,7 +704,10 @@ fa_fwd_dma_kernel(KernelArgs p) {
     const char *vg = p.v + 2 * (bb * p.v_sb + hh * p.v_sh);
 
     const int kv_end = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
-    const int n_tiles = (kv_end + BN - 1) / BN;
+    // KV tiles [t_begin, n_tiles) of this unit: the whole range, or one run
+    // of split_tiles tiles under split-KV (possibly empty past the diagonal).
+    const int t_begin = split * p.split_tiles;
+    const int n_tiles = min((kv_end + BN - 1) / BN, t_begin + p.split_tiles);
     const int wave_last_q = q0w + 31;
 
     // DMA of KV tile t into stage STG: instruction i < 2*IPW of this wave
@@ -710,12 +729,17 @@ fa_fwd_dma_kernel(KernelArgs p) {
       dma16_lds((i & 1) ? rv : rk, base + (i & 1) * C::TILE + (wave + j * NW) * 1024, (i & 1) ? dv[j] : dk[j]);
     };
 
-    // Prologue: KV tile 0 into stage 0.
+    // Prologue: KV tile t_begin into its stage (t_begin & 1).
     {
       BufRsrc rk, rv;
-      tile_rsrc(0, &rk, &rv);
+      tile_rsrc(t_begin, &rk, &rv);
+      if (t_begin & 1) {
 #pragma unroll
-      for (int i = 0; i < 2 * C::IPW; ++i) dma(std::integral_constant<int, 0>{}, rk, rv, i);
+        for (int i = 0; i < 2 * C::IPW; ++i) dma(std::integral_constant<int, 1>{}, rk, rv, i);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 2 * C::IPW; ++i) dma(std::integral_constant<int, 0>{}, rk, rv, i);
+      }
     }
 
     u32x4_t qf[D / 16];
@@ -914,7 +938,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
     n_full = min(n_full, n_tiles);
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
-    int t = 0;
+    int t = t_begin;
     auto run = [&](int end, auto masked_tag) __attribute__((always_inline)) {
       if (t < end && (t & 1)) kv_tile(t++, masked_tag, S1{});
       for (; t + 1 < end; t += 2) {
@@ -930,6 +954,28 @@ fa_fwd_dma_kernel(KernelArgs p) {
 #endif
 
     const float l_tot = halves_sum(l_run);
+    if (p.kv_splits > 1) {
+      // Partial result of this KV run: O normalised by its own row sum, in
+      // fp32, and its natural-log LSE (-inf, with O = 0, where no key of the
+      // run is visible to the row).
+      const float inv_p = l_tot > 0.f ? 1.f / l_tot : 0.f;
+      const int64_t unit = (int64_t)split * p.B * p.H + bh;
+      const BufRsrc rpo = make_rsrc(p.part_o + unit * p.Sq * D, (uint32_t)((int64_t)p.Sq * D * 4));
+      const uint32_t po = (uint32_t)(qrow * D * 4 + 16 * h);
+#pragma unroll
+      for (int db = 0; db < C::DB; ++db)
+#pragma unroll
+        for (int j = 0; j < (D >= 32 ? 4 : 2); ++j) {
+          u32x4_t x;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[i] = __builtin_bit_cast(uint32_t, oacc[db][4 * j + i] * inv_p);
+          buf_store16(x, rpo, po + 4 * (32 * db + 8 * j));
+        }
+      const uint32_t nbytes = (uint32_t)p.Sq * 4u;
+      const BufRsrc rpl = make_rsrc(p.part_lse + unit * p.Sq, nbytes);
+      const float lse = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
+      buf_store4(__builtin_bit_cast(uint32_t, lse), rpl, h ? nbytes : (uint32_t)qrow * 4u);
+    } else {
     const float inv = 1.f / l_tot;
     {
       const char *og = p.o + 2 * (bb * p.o_sb + hh * p.o_sh);
@@ -950,6 +996,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
       const BufRsrc rl = make_rsrc(p.lse + ((int64_t)bb * p.H + hh) * p.Sq, nbytes);
       const float lse = (m_run + __log2f(l_tot)) * kLn2;
       buf_store4(__builtin_bit_cast(uint32_t, lse), rl, h ? nbytes : (uint32_t)qrow * 4u);
+    }
     }
 #ifdef FA_TIMING
     if (p.timing != nullptr && lane == 0) {
@@ -1054,9 +1101,9 @@ fa_fwd_pp_kernel(KernelArgs p) {
   // of a tile and published through LDS at its end, behind a barrier).
   __shared__ uint32_t s_ticket[2];
   const TileQueue tq(p);
-  int bh, mt;
+  int bh, mt, split;
   for (int it = 0; tq.tile(it == 0 ? tq.first() : s_ticket[it & 1], p.n_mtiles, CAUSAL, p.q_group, p.q_bands,
-                           &bh, &mt);
+                           &bh, &mt, &split);
        ++it) {
     unsigned long long next_raw = 0;
     if (threadIdx.x == 0) next_raw = tq.request();
@@ -1391,6 +1438,60 @@ fa_fwd_pp_kernel(KernelArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Split-KV merge.  One wave per (b, h, row): with m = max_s LSE_s and
+// w_s = exp(LSE_s - m),
+//     LSE = m + ln(sum_s w_s),   O = sum_s w_s O_s / sum_s w_s,
+// exact for partial results normalised by their own row sums (O_s) with
+// natural-log LSE_s; runs with no visible key have LSE_s = -inf, w_s = 0.
+// HBM-bound: reads splits * (D + 1) fp32 per row, writes D halves + 1 fp32.
+struct MergeArgs {
+  const float *part_o;   // [splits][B*H][Sq][D]
+  const float *part_lse; // [splits][B*H][Sq]
+  char *o;
+  float *lse;            // may be null
+  int64_t o_sb, o_sh, o_ss;
+  int32_t B, H, Sq, D, splits;
+};
+
+template <bool BF16>
+__global__ void __launch_bounds__(256) fa_merge_kernel(MergeArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t rows = (int64_t)a.B * a.H * a.Sq;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= rows) return;
+  const int bh = (int)(row / a.Sq);
+  const int q = (int)(row - (int64_t)bh * a.Sq);
+  const int64_t plane = rows;  // rows per split
+  float m = -INFINITY;
+  for (int s = 0; s < a.splits; ++s) m = fmaxf(m, a.part_lse[s * plane + row]);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float wsum = 0.f;
+  for (int s = 0; s < a.splits; ++s) {
+    const float ls = a.part_lse[s * plane + row];
+    const float w = ls == -INFINITY ? 0.f : fast_exp2((ls - m) * kLog2e);
+    wsum += w;
+    const float *src = a.part_o + (s * plane + row) * a.D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = lane + 64 * i;
+      if (d < a.D) acc[i] += w * src[d];
+    }
+  }
+  const float inv = 1.f / wsum;
+  const int bb = bh / a.H, hh = bh - bb * a.H;
+  char *dst = a.o + 2 * (bb * a.o_sb + hh * a.o_sh + (int64_t)q * a.o_ss);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = lane + 64 * i;
+    if (d < a.D) {
+      const uint32_t v = pack2<BF16>(acc[i] * inv, 0.f);
+      *(uint16_t *)(dst + 2 * d) = (uint16_t)(v & 0xffffu);
+    }
+  }
+  if (a.lse != nullptr && lane == 0) a.lse[row] = m + __logf(wsum);
+}
+
+// ---------------------------------------------------------------------------
 // Kernel table.
 typedef void (*KernelFn)(KernelArgs);
 
@@ -1399,20 +1500,21 @@ struct KernelEntry {
   int32_t stages;     // LDS stages of the DMA kernel; 0 = register-staged kernel
   int32_t lds_bytes;
   int32_t wg_per_cu;  // resident workgroups per CU (registers and LDS)
+  bool splittable;    // supports split-KV (partial outputs + merge)
   KernelFn fn;
 };
 
 template <int D, int BN, int NW, bool BF16, bool CAUSAL>
 constexpr KernelEntry entry() {
   return KernelEntry{D, BF16 ? 1 : 0, CAUSAL ? 1 : 0, BN, NW, 0,
-                     FaConfig<D, BN, NW, BF16, CAUSAL>::LDS_BYTES, 8 / NW,
+                     FaConfig<D, BN, NW, BF16, CAUSAL>::LDS_BYTES, 8 / NW, false,
                      fa_fwd_kernel<D, BN, NW, BF16, CAUSAL>};
 }
 
 template <int D, int BN, int NW, int NSTAGE, int OCC, bool BF16, bool CAUSAL>
 constexpr KernelEntry entry_dma() {
   return KernelEntry{D, BF16 ? 1 : 0, CAUSAL ? 1 : 0, BN, NW, NSTAGE,
-                     Cfg2<D, BN, NW, NSTAGE, OCC>::LDS_BYTES, OCC,
+                     Cfg2<D, BN, NW, NSTAGE, OCC>::LDS_BYTES, OCC, true,
                      fa_fwd_dma_kernel<D, BN, NW, NSTAGE, OCC, BF16, CAUSAL>};
 }
 
@@ -1420,10 +1522,10 @@ constexpr KernelEntry entry_dma() {
   entry<D, BN, NW, false, false>(), entry<D, BN, NW, false, true>(),                 \
       entry<D, BN, NW, true, false>(), entry<D, BN, NW, true, true>()
 #define FA_PP_ENTRIES(D, BN, NR)                                                                     \
-  KernelEntry{D, 0, 0, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, fa_fwd_pp_kernel<D, BN, NR, false, false>}, \
-  KernelEntry{D, 0, 1, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, fa_fwd_pp_kernel<D, BN, NR, false, true>},  \
-  KernelEntry{D, 1, 0, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, fa_fwd_pp_kernel<D, BN, NR, true, false>},  \
-  KernelEntry{D, 1, 1, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, fa_fwd_pp_kernel<D, BN, NR, true, true>}
+  KernelEntry{D, 0, 0, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, false, fa_fwd_pp_kernel<D, BN, NR, false, false>}, \
+  KernelEntry{D, 0, 1, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, false, fa_fwd_pp_kernel<D, BN, NR, false, true>},  \
+  KernelEntry{D, 1, 0, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, false, fa_fwd_pp_kernel<D, BN, NR, true, false>},  \
+  KernelEntry{D, 1, 1, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, false, fa_fwd_pp_kernel<D, BN, NR, true, true>}
 #define FA_DMA_ENTRIES(D, BN, NW, ST, OCC)                                                     \
   entry_dma<D, BN, NW, ST, OCC, false, false>(), entry_dma<D, BN, NW, ST, OCC, false, true>(), \
       entry_dma<D, BN, NW, ST, OCC, true, false>(), entry_dma<D, BN, NW, ST, OCC, true, true>()
@@ -1469,14 +1571,17 @@ struct Plan {
   int kernel;
   int BM, BN, NW;
   int n_mtiles;
-  int64_t total_tiles;
+  int64_t total_tiles;  // (head, m-tile) tiles
   int grid;
+  int split_tiles;      // KV tiles per split-KV run (0: no split)
 };
+
+constexpr int kMaxKvSplits = 64;
 
 // CUs of an MI355X; fa_fwd asks the device, the host-only calls assume this.
 constexpr int kDefaultCuCount = 256;
 
-int make_plan(const fa_fwd_params *p, Plan *out, int cu_count = kDefaultCuCount) {
+int make_plan(const fa_fwd_params *p, Plan *out, int cu_count = kDefaultCuCount, int splits = 1) {
   int bn, nw;
   if (p->block_m == 0 && p->block_n == 0) {
     default_tiling(p->D, p->dtype, p->causal, &bn, &nw);
@@ -1498,9 +1603,13 @@ int make_plan(const fa_fwd_params *p, Plan *out, int cu_count = kDefaultCuCount)
   // kernel runs two waves per SIMD, so 8 / NW workgroups per CU), pulling
   // tiles from the tile queues; PERSISTENT_PROGRAMS (num_programs) overrides
   // the count.
+  const int64_t kv_tiles = ((int64_t)p->Sk + bn - 1) / bn;
+  out->split_tiles = splits > 1 ? (int)((kv_tiles + splits - 1) / splits) : 0;
+  const int64_t units = out->total_tiles * (splits > 1 ? splits : 1);
+  if (units > INT32_MAX) return FA_ERR_SHAPE;
   int64_t grid = (int64_t)kKernels[kid].wg_per_cu * (cu_count > 0 ? cu_count : kDefaultCuCount);
   if (p->num_programs > 0) grid = p->num_programs;
-  if (grid > out->total_tiles) grid = out->total_tiles;
+  if (grid > units) grid = units;
   out->grid = (int)grid;
   return FA_OK;
 }
@@ -1533,6 +1642,119 @@ extern "C" void fa_set_timing_buffer(void *p) { g_timing_buffer = (uint32_t *)p;
 #else
 static uint32_t *const g_timing_buffer = nullptr;
 #endif
+
+namespace {
+
+// Workspace of a split-KV launch: partial O, then (256-byte aligned) LSE.
+int64_t split_part_o_bytes(const fa_fwd_params *p, int splits) {
+  return (((int64_t)splits * p->B * p->H * p->Sq * p->D * 4) + 255) / 256 * 256;
+}
+int64_t split_workspace_bytes(const fa_fwd_params *p, int splits) {
+  return split_part_o_bytes(p, splits) + (int64_t)splits * p->B * p->H * p->Sq * 4;
+}
+
+int launch(const fa_fwd_params *p, void *hip_stream, int splits, void *workspace, int64_t workspace_bytes) {
+  const int rc = fa_validate(p);
+  if (rc != FA_OK) return rc;
+  if (p->B == 0 || p->H == 0 || p->Sq == 0) return FA_OK;
+  int device = 0, cu_count = 0;
+  if (hipGetDevice(&device) != hipSuccess ||
+      hipDeviceGetAttribute(&cu_count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    cu_count = kDefaultCuCount;
+  Plan plan;
+  const int prc = make_plan(p, &plan, cu_count, splits);
+  if (prc != FA_OK) return prc;
+  const KernelEntry &e = kKernels[plan.kernel];
+  if (splits > 1) {
+    if (!e.splittable) return FA_ERR_TILING;
+    if (workspace == nullptr) return FA_ERR_NULL;
+    if (((uintptr_t)workspace & 255u) != 0) return FA_ERR_ALIGN;
+    if (workspace_bytes < split_workspace_bytes(p, splits)) return FA_ERR_SHAPE;
+  }
+
+  KernelArgs a;
+  a.q = (const char *)p->q;
+  a.k = (const char *)p->k;
+  a.v = (const char *)p->v;
+  a.o = (char *)p->o;
+  a.lse = p->lse;
+  a.q_sb = p->q_stride[0]; a.q_sh = p->q_stride[1]; a.q_ss = p->q_stride[2];
+  a.k_sb = p->k_stride[0]; a.k_sh = p->k_stride[1]; a.k_ss = p->k_stride[2];
+  a.v_sb = p->v_stride[0]; a.v_sh = p->v_stride[1]; a.v_ss = p->v_stride[2];
+  a.o_sb = p->o_stride[0]; a.o_sh = p->o_stride[1]; a.o_ss = p->o_stride[2];
+  a.B = p->B;
+  a.H = p->H;
+  a.Sq = p->Sq;
+  a.Sk = p->Sk;
+  a.n_mtiles = plan.n_mtiles;
+  a.total_tiles = (int32_t)plan.total_tiles;
+  a.kv_splits = splits > 1 ? splits : 1;
+  a.split_tiles = splits > 1 ? plan.split_tiles : (1 << 30);
+  a.part_o = splits > 1 ? (float *)workspace : nullptr;
+  a.part_lse = splits > 1 ? (float *)((char *)workspace + split_part_o_bytes(p, splits)) : nullptr;
+  {
+    unsigned long long *base = queue_base(device);
+    if (base == nullptr) return FA_ERR_LAUNCH;
+    const unsigned long long seq = g_launch_seq.fetch_add(1, std::memory_order_relaxed);
+    a.queue = base + (seq % kQueueSlots) * kQueues * kQueueStride;
+    const int64_t bh = (int64_t)p->B * p->H;
+    int64_t nq = kQueues;
+    if (nq > plan.grid) nq = plan.grid;
+    if (nq > bh) nq = bh;
+    a.nq = (int32_t)nq;
+    // Queue order: all of a queue's heads at once (heaviest first across
+    // them) while their K+V fit in 16 MiB of L2 + MALL reuse distance;
+    // otherwise groups small enough for that, but at least large enough that
+    // a group has ~4 tiles per worker, in two weight bands.  Measured on the
+    // five benchmark workloads (within 1-3% of the best fixed choice each).
+    const int64_t nh = (bh + nq - 1) / nq;  // heads of queue 0
+    const int64_t workers = plan.grid / nq;
+    const int64_t kv_head = (int64_t)p->Sk * p->D * 2 * 2;
+    const int64_t budget = (int64_t)16 << 20;
+    int64_t group = nh;
+    if (nh * kv_head > budget) {
+      const int64_t by_l2 = budget / kv_head > 1 ? budget / kv_head : 1;
+      const int64_t by_work = (4 * workers + plan.n_mtiles - 1) / plan.n_mtiles;
+      group = by_l2 > by_work ? by_l2 : by_work;
+      if (group > nh) group = nh;
+      if (group > by_l2 && by_l2 * 2 >= by_work) group = by_l2;
+    }
+    a.q_group = (int32_t)(group > 0 ? group : 1);
+    a.q_bands = 2;
+  }
+  // A negative scale is folded into Q (sign flip of every element, exact),
+  // a zero scale into a tiny positive one (all logits ~0: uniform weights).
+  const float s = p->sm_scale;
+  a.q_sign = s < 0.f ? 0x80008000u : 0u;
+  float c = fabsf(s) * kLog2e;
+  if (c < 1e-30f) c = 1e-30f;
+  a.c = c;
+  a.timing = g_timing_buffer;
+
+  hipStream_t stream = (hipStream_t)hip_stream;
+  hipLaunchKernelGGL(e.fn, dim3(plan.grid), dim3(64 * e.NW), 0, stream, a);
+  if (hipGetLastError() != hipSuccess) return FA_ERR_LAUNCH;
+  if (splits > 1) {
+    MergeArgs m;
+    m.part_o = a.part_o;
+    m.part_lse = a.part_lse;
+    m.o = a.o;
+    m.lse = a.lse;
+    m.o_sb = a.o_sb; m.o_sh = a.o_sh; m.o_ss = a.o_ss;
+    m.B = p->B; m.H = p->H; m.Sq = p->Sq; m.D = p->D; m.splits = splits;
+    const int64_t rows = (int64_t)p->B * p->H * p->Sq;
+    const unsigned blocks = (unsigned)((rows + 3) / 4);
+    if (p->dtype == FA_DTYPE_BF16) {
+      hipLaunchKernelGGL(fa_merge_kernel<true>, dim3(blocks), dim3(256), 0, stream, m);
+    } else {
+      hipLaunchKernelGGL(fa_merge_kernel<false>, dim3(blocks), dim3(256), 0, stream, m);
+    }
+    if (hipGetLastError() != hipSuccess) return FA_ERR_LAUNCH;
+  }
+  return FA_OK;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -1625,82 +1847,38 @@ int fa_kernel_info(int index, int32_t out[6]) {
   return FA_OK;
 }
 
-int fa_fwd(const fa_fwd_params *p, void *hip_stream) {
-  const int rc = fa_validate(p);
-  if (rc != FA_OK) return rc;
-  if (p->B == 0 || p->H == 0 || p->Sq == 0) return FA_OK;
-  int device = 0, cu_count = 0;
-  if (hipGetDevice(&device) != hipSuccess ||
-      hipDeviceGetAttribute(&cu_count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
-    cu_count = kDefaultCuCount;
+int fa_fwd(const fa_fwd_params *p, void *hip_stream) { return launch(p, hip_stream, 1, nullptr, 0); }
+
+int64_t fa_split_workspace_bytes(const fa_fwd_params *p, int32_t kv_splits) {
+  if (p == nullptr) return FA_ERR_NULL;
+  if (kv_splits < 1 || kv_splits > kMaxKvSplits) return FA_ERR_GRID;
+  if (p->B < 0 || p->H < 0 || p->Sq < 0 || p->D <= 0) return FA_ERR_SHAPE;
+  return kv_splits == 1 ? 0 : split_workspace_bytes(p, kv_splits);
+}
+
+int fa_fwd_split(const fa_fwd_params *p, int32_t kv_splits, void *workspace, int64_t workspace_bytes,
+                 void *hip_stream) {
+  if (kv_splits < 1 || kv_splits > kMaxKvSplits) return FA_ERR_GRID;
+  return launch(p, hip_stream, kv_splits, workspace, workspace_bytes);
+}
+
+int32_t fa_default_kv_splits(const fa_fwd_params *p) {
+  // Shape-only (no pointer or stride checks): usable before tensors exist.
+  if (p == nullptr || p->B <= 0 || p->H <= 0 || p->Sq <= 0 || p->Sk <= 0) return 1;
+  if (!is_supported_head_dim(p->D) || (p->dtype != FA_DTYPE_FP16 && p->dtype != FA_DTYPE_BF16)) return 1;
   Plan plan;
-  const int prc = make_plan(p, &plan, cu_count);
-  if (prc != FA_OK) return prc;
-
-  KernelArgs a;
-  a.q = (const char *)p->q;
-  a.k = (const char *)p->k;
-  a.v = (const char *)p->v;
-  a.o = (char *)p->o;
-  a.lse = p->lse;
-  a.q_sb = p->q_stride[0]; a.q_sh = p->q_stride[1]; a.q_ss = p->q_stride[2];
-  a.k_sb = p->k_stride[0]; a.k_sh = p->k_stride[1]; a.k_ss = p->k_stride[2];
-  a.v_sb = p->v_stride[0]; a.v_sh = p->v_stride[1]; a.v_ss = p->v_stride[2];
-  a.o_sb = p->o_stride[0]; a.o_sh = p->o_stride[1]; a.o_ss = p->o_stride[2];
-  a.B = p->B;
-  a.H = p->H;
-  a.Sq = p->Sq;
-  a.Sk = p->Sk;
-  a.n_mtiles = plan.n_mtiles;
-  a.total_tiles = (int32_t)plan.total_tiles;
-  {
-    unsigned long long *base = queue_base(device);
-    if (base == nullptr) return FA_ERR_LAUNCH;
-    const unsigned long long seq = g_launch_seq.fetch_add(1, std::memory_order_relaxed);
-    a.queue = base + (seq % kQueueSlots) * kQueues * kQueueStride;
-    const int64_t bh = (int64_t)p->B * p->H;
-    int64_t nq = kQueues;
-    if (nq > plan.grid) nq = plan.grid;
-    if (nq > bh) nq = bh;
-    a.nq = (int32_t)nq;
-    // Queue order: all of a queue's heads at once (heaviest first across
-    // them) while their K+V fit in 16 MiB of L2 + MALL reuse distance;
-    // otherwise groups small enough for that, but at least large enough that
-    // a group has ~4 tiles per worker, in two weight bands.  Measured on the
-    // five benchmark workloads (within 1-3% of the best fixed choice each).
-    const int64_t nh = (bh + nq - 1) / nq;  // heads of queue 0
-    const int64_t workers = plan.grid / nq;
-    const int64_t kv_head = (int64_t)p->Sk * p->D * 2 * 2;
-    const int64_t budget = (int64_t)16 << 20;
-    int64_t group = nh;
-    if (nh * kv_head > budget) {
-      const int64_t by_l2 = budget / kv_head > 1 ? budget / kv_head : 1;
-      const int64_t by_work = (4 * workers + plan.n_mtiles - 1) / plan.n_mtiles;
-      group = by_l2 > by_work ? by_l2 : by_work;
-      if (group > nh) group = nh;
-      if (group > by_l2 && by_l2 * 2 >= by_work) group = by_l2;
-    }
-    a.q_group = (int32_t)(group > 0 ? group : 1);
-    a.q_bands = 2;
-#ifdef FA_DEV_KNOBS
-    if (const char *e = getenv("FA_QG")) a.q_group = atoi(e) > 0 ? atoi(e) : a.q_group;
-    if (const char *e = getenv("FA_QB")) a.q_bands = atoi(e) > 0 ? atoi(e) : 1;
-#endif
-  }
-  // A negative scale is folded into Q (sign flip of every element, exact),
-  // a zero scale into a tiny positive one (all logits ~0: uniform weights).
-  const float s = p->sm_scale;
-  a.q_sign = s < 0.f ? 0x80008000u : 0u;
-  float c = fabsf(s) * kLog2e;
-  if (c < 1e-30f) c = 1e-30f;
-  a.c = c;
-  a.timing = g_timing_buffer;
-
+  if (make_plan(p, &plan) != FA_OK) return 1;
   const KernelEntry &e = kKernels[plan.kernel];
-  hipStream_t stream = (hipStream_t)hip_stream;
-  hipLaunchKernelGGL(e.fn, dim3(plan.grid), dim3(64 * e.NW), 0, stream, a);
-  const hipError_t err = hipGetLastError();
-  return err == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
+  if (!e.splittable) return 1;
+  // Split only a grid that would leave most workgroup slots empty, and only
+  // into runs of at least 8 KV tiles (the merge costs an extra HBM pass).
+  const int64_t slots = (int64_t)e.wg_per_cu * kDefaultCuCount;
+  if (plan.total_tiles * 2 > slots) return 1;
+  const int64_t kv_tiles = ((int64_t)p->Sk + plan.BN - 1) / plan.BN;
+  int64_t splits = (slots + plan.total_tiles - 1) / plan.total_tiles;
+  if (splits > kv_tiles / 8) splits = kv_tiles / 8;
+  if (splits > kMaxKvSplits) splits = kMaxKvSplits;
+  return splits > 1 ? (int32_t)splits : 1;
 }
 
 }  // extern "C"

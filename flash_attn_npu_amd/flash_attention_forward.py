@@ -37,6 +37,9 @@ RESULT_DIR_NAME = "result_dir"
 # way every workgroup walks its share of the balanced tile schedule (the
 # reference's persistent grid, flash_attention_forward.py:24,616-623).
 DEFAULT_PERSISTENT_PROGRAMS = 0
+# 0 = the library's split-KV choice (fa_default_kv_splits: only grids that
+# would leave most workgroup slots empty); KV_SPLITS in [1, 64] overrides.
+DEFAULT_KV_SPLITS = 0
 PROFILE_OP_NAME = "fa_fwd_kernel"
 LIB_NAME = "libfa_mi355x.so"
 SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
@@ -133,6 +136,12 @@ def _load_library():
     lib.fa_kernel_info.restype = ctypes.c_int
     lib.fa_params_size.argtypes = []
     lib.fa_params_size.restype = ctypes.c_int
+    lib.fa_split_workspace_bytes.argtypes = [P, ctypes.c_int32]
+    lib.fa_split_workspace_bytes.restype = ctypes.c_int64
+    lib.fa_fwd_split.argtypes = [P, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    lib.fa_fwd_split.restype = ctypes.c_int
+    lib.fa_default_kv_splits.argtypes = [P]
+    lib.fa_default_kv_splits.restype = ctypes.c_int32
     if lib.fa_params_size() != ctypes.sizeof(FaFwdParams):
         raise RuntimeError("fa_fwd_params layout mismatch between the library and this binding")
     _LIB = lib
@@ -162,6 +171,17 @@ def kernel_table():
 
 # --------------------------------------------------------------------------
 # Tiling policy (flash_attention_forward.py:156-252, 616-644)
+
+def _get_kv_splits():
+    """Split-KV factor from $KV_SPLITS (1 = never split), else 0 = the library's choice."""
+    raw = os.environ.get("KV_SPLITS")
+    if raw is None:
+        return DEFAULT_KV_SPLITS
+    value = int(raw)
+    if not 1 <= value <= 64:
+        raise ValueError("KV_SPLITS must be in [1, 64]")
+    return value
+
 
 def _get_persistent_programs():
     """Program count from $PERSISTENT_PROGRAMS (>= 1), else 0 = the library's resident grid.
@@ -227,6 +247,11 @@ def _describe_runtime(z, h, n_ctx, head_dim, causal, bm=None, bn=None):
     block_m, block_n, tiling_source = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn)
     cfg = _query_config(z, h, n_ctx, head_dim, causal, block_m, block_n,
                         programs=_get_persistent_programs())
+    splits = _get_kv_splits()
+    if splits == 0:
+        p = _shape_params(z, h, n_ctx, head_dim, causal, block_m, block_n, torch.float16,
+                          _get_persistent_programs())
+        splits = int(_load_library().fa_default_kv_splits(ctypes.byref(p)))
     return {
         "selected_config": {"BLOCK_M": cfg[0], "BLOCK_N": cfg[1]},
         "tiling_source": tiling_source,
@@ -236,6 +261,7 @@ def _describe_runtime(z, h, n_ctx, head_dim, causal, bm=None, bn=None):
         "waves": cfg[2],
         "lds_bytes": cfg[5],
         "kernel_id": cfg[7],
+        "kv_splits": splits,
     }
 
 
@@ -307,9 +333,19 @@ def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
     p.sm_scale = sm_scale
     p.block_m, p.block_n = int(bm), int(bn)
     p.num_programs = _get_persistent_programs()
+    splits = _get_kv_splits()
+    if splits == 0:
+        splits = int(lib.fa_default_kv_splits(ctypes.byref(p)))
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
-        _check(lib.fa_fwd(ctypes.byref(p), ctypes.c_void_p(stream)), "fa_fwd")
+        if splits > 1:
+            nbytes = int(lib.fa_split_workspace_bytes(ctypes.byref(p), splits))
+            _check(nbytes if nbytes < 0 else 0, "fa_split_workspace_bytes")
+            workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)  # caching allocator: 512 B aligned
+            _check(lib.fa_fwd_split(ctypes.byref(p), splits, ctypes.c_void_p(workspace.data_ptr()), nbytes,
+                                    ctypes.c_void_p(stream)), "fa_fwd_split")
+        else:
+            _check(lib.fa_fwd(ctypes.byref(p), ctypes.c_void_p(stream)), "fa_fwd")
     return out, lse
 
 

@@ -125,6 +125,31 @@ int fa_kernel_info(int index, int32_t out[6]);
  * (ctypes, cffi) can check its struct layout before the first call. */
 int fa_params_size(void);
 
+/* ---- Split-KV.  No counterpart in the reference (its grid is one program per
+ * (z, h, m-tile), flash_attention_forward.py:1125-1127).  For shapes whose
+ * (head, m-tile) tiles leave most of the GPU idle (few heads, long sequences),
+ * every m-tile's KV range is cut into kv_splits runs computed in parallel;
+ * each run writes a partial O (fp32, normalised by its own row sum) and its
+ * LSE into `workspace`, and a merge kernel combines them on the same stream:
+ *     LSE = m + ln sum_s exp(LSE_s - m),  O = sum_s exp(LSE_s - LSE) O_s.
+ * Results match fa_fwd within rounding (the sums are grouped differently). */
+
+/* Workspace bytes fa_fwd_split needs for kv_splits (0 when kv_splits == 1);
+ * negative FA_ERR_* on bad arguments. */
+int64_t fa_split_workspace_bytes(const fa_fwd_params *p, int32_t kv_splits);
+
+/* fa_fwd with the KV range split kv_splits ways (1 <= kv_splits <= 64).
+ * workspace: device memory of at least fa_split_workspace_bytes bytes,
+ * 256-byte aligned, owned by the caller and not read after the call's work
+ * completes on the stream.  FA_ERR_TILING if the selected kernel cannot split. */
+int fa_fwd_split(const fa_fwd_params *p, int32_t kv_splits, void *workspace, int64_t workspace_bytes,
+                 void *hip_stream);
+
+/* The library's split choice for these parameters: > 1 only when the
+ * unsplit grid would fill less than half of the resident workgroup slots and
+ * each run keeps at least 8 KV tiles.  Host-only. */
+int32_t fa_default_kv_splits(const fa_fwd_params *p);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,6 +26,15 @@ key j is visible to query i iff j <= i.
 float64 with math.exp (a different algorithm: explicit loops, no BLAS); it is
 used on tiny inputs to pin `attention_ref`.
 
+`attention_partial` / `merge_partials` restate the split-KV path, which has no
+counterpart in the reference: attention over a key range [lo, hi) only (O
+normalised by that range's own row sum, LSE over that range, -inf and O = 0
+for rows that see no key there), and the exact LSE-weighted merge
+    LSE = m + log sum_s exp(LSE_s - m),  O = sum_s exp(LSE_s - LSE) O_s,
+with m = max_s LSE_s.  They are pinned by the partition identity: merging the
+partials of any partition of the keys reproduces attention_ref
+(tests/test_oracle.py, including mutants of the merge).
+
 Rounding helpers produce the fp16 / bf16 values the GPU path writes, so that
 an output can be compared to the oracle after the same final cast the
 reference applies (`.to(q.dtype)`, evaluate_attention.py:143).
@@ -48,6 +57,8 @@ import numpy as np
 __all__ = [
     "attention_ref",
     "attention_bruteforce",
+    "attention_partial",
+    "merge_partials",
     "round_bf16",
     "round_fp16",
     "round_to",
@@ -166,6 +177,61 @@ def attention_bruteforce(q, k, v, causal: bool, sm_scale: float):
             for t in range(v.shape[1]):
                 out[i, t] += w * v[j, t]
     return out, lse
+
+
+def attention_partial(q, k, v, causal: bool, sm_scale: float, lo: int, hi: int):
+    """Attention over keys [lo, hi) only: (O_part float32, LSE_part float32).
+
+    Same shapes and causal convention as attention_ref (key j visible to query
+    i iff j <= i); O_part is normalised by the range's own row sum; rows that
+    see no key of the range get O_part = 0 and LSE_part = -inf.
+    """
+    q = np.asarray(q, dtype=np.float32)
+    k = np.asarray(k, dtype=np.float32)
+    v = np.asarray(v, dtype=np.float32)
+    sq, sk = q.shape[-2], k.shape[-2]
+    lead = q.shape[:-2]
+    qf = q.reshape(-1, sq, q.shape[-1])
+    kf = k.reshape(-1, sk, k.shape[-1])
+    vf = v.reshape(-1, sk, v.shape[-1])
+    out = np.zeros((qf.shape[0], sq, vf.shape[-1]), dtype=np.float32)
+    lse = np.full((qf.shape[0], sq), -np.inf, dtype=np.float32)
+    keys = np.arange(lo, min(hi, sk))
+    if keys.size == 0:
+        return out.reshape(*lead, sq, -1), lse.reshape(*lead, sq)
+    visible = np.ones((sq, keys.size), dtype=bool)
+    if causal:
+        visible = keys[None, :] <= np.arange(sq)[:, None]
+    for i in range(qf.shape[0]):
+        scores = (qf[i] @ kf[i][keys].T) * np.float32(sm_scale)
+        scores = np.where(visible, scores, np.float32(-np.inf))
+        row_max = scores.max(axis=-1, keepdims=True)
+        seen = np.isfinite(row_max[..., 0])
+        safe_max = np.where(np.isfinite(row_max), row_max, np.float32(0))
+        e = np.exp(scores - safe_max)
+        denom = e.sum(axis=-1, keepdims=True)
+        o = (e / np.where(denom > 0, denom, 1)) @ vf[i][keys]
+        out[i] = np.where(seen[:, None], o, 0).astype(np.float32)
+        lse[i] = np.where(seen, np.log(np.where(denom[..., 0] > 0, denom[..., 0], 1)) + safe_max[..., 0],
+                          -np.inf).astype(np.float32)
+    return out.reshape(*lead, sq, -1), lse.reshape(*lead, sq)
+
+
+def merge_partials(parts):
+    """Exact LSE-weighted merge of [(O_s, LSE_s), ...] -> (O, LSE), float32.
+
+    m = max_s LSE_s;  w_s = exp(LSE_s - m) (0 where LSE_s = -inf);
+    LSE = m + log(sum_s w_s);  O = sum_s w_s O_s / sum_s w_s.
+    """
+    lses = np.stack([np.asarray(l, dtype=np.float64) for _, l in parts])
+    outs = np.stack([np.asarray(o, dtype=np.float64) for o, _ in parts])
+    m = lses.max(axis=0)
+    safe_m = np.where(np.isfinite(m), m, 0.0)
+    w = np.where(np.isfinite(lses), np.exp(lses - safe_m), 0.0)
+    wsum = w.sum(axis=0)
+    o = (w[..., None] * outs).sum(axis=0) / np.where(wsum > 0, wsum, 1.0)[..., None]
+    lse = np.where(wsum > 0, safe_m + np.log(np.where(wsum > 0, wsum, 1.0)), -np.inf)
+    return o.astype(np.float32), lse.astype(np.float32)
 
 
 def attention_flops(b: int, h: int, sq: int, sk: int, d: int, causal: bool) -> float:

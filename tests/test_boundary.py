@@ -263,3 +263,30 @@ def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, str(REPO / "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True, timeout=60)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+# ---------------------------------------------------------------------------
+# Split-KV host logic (no launch)
+
+def test_split_workspace_bytes(lib):
+    p = _params(shape=(2, 3, 100, 64))
+    part_o = 4 * 2 * 3 * 100 * 64 * 4
+    assert lib.fa_split_workspace_bytes(ctypes.byref(p), 4) == (part_o + 255) // 256 * 256 + 4 * 2 * 3 * 100 * 4
+    assert lib.fa_split_workspace_bytes(ctypes.byref(p), 1) == 0
+    assert lib.fa_split_workspace_bytes(ctypes.byref(p), 0) == -9
+    assert lib.fa_split_workspace_bytes(ctypes.byref(p), 65) == -9
+
+
+@pytest.mark.parametrize("shape,splits", [((1, 1, 4096, 128), 8), ((1, 8, 512, 64), 1), ((4, 32, 2048, 128), 1),
+                                          ((1, 1, 16384, 64), 4), ((1, 1, 300, 64), 1)])
+def test_default_kv_splits(lib, shape, splits):
+    p = _params(shape=shape, causal=0)
+    assert lib.fa_default_kv_splits(ctypes.byref(p)) == splits
+
+
+def test_split_argument_errors_before_launch(lib):
+    p = _params(shape=(1, 2, 700, 128))
+    assert lib.fa_fwd_split(ctypes.byref(p), 0, None, 0, None) == -9
+    assert lib.fa_fwd_split(ctypes.byref(p), 4, None, 1 << 20, None) == -1
+    assert lib.fa_fwd_split(ctypes.byref(p), 4, (1 << 40), 16, None) == -2
+    assert lib.fa_fwd_split(ctypes.byref(p), 4, (1 << 40) + 64, 1 << 30, None) == -6

@@ -249,3 +249,76 @@ def test_rejects_mismatched_shapes():
         attention_ref(rand(4, 8), rand(4, 16), rand(4, 16), False, 1.0)
     with pytest.raises(ValueError):
         attention_ref(rand(2, 4, 8), rand(3, 4, 8), rand(3, 4, 8), False, 1.0)
+
+
+# ---------------------------------------------------------------------------
+# Split-KV restatement: partial attention over key ranges + LSE merge.
+
+from oracle.attention_oracle import attention_partial, merge_partials  # noqa: E402
+
+
+def _partition_check(merge, partial=attention_partial, seed=5, sq=37, sk=37, d=16, causal=True,
+                     cuts=(0, 5, 16, 30, 37), scale=0.3):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((2, sq, d)).astype(np.float32)
+    k = rng.standard_normal((2, sk, d)).astype(np.float32)
+    v = rng.standard_normal((2, sk, d)).astype(np.float32)
+    want_o, want_l = attention_ref(q, k, v, causal, scale)
+    parts = [partial(q, k, v, causal, scale, lo, hi) for lo, hi in zip(cuts[:-1], cuts[1:])]
+    with np.errstate(over="ignore", invalid="ignore"):
+        got_o, got_l = merge(parts)
+    return float(np.nan_to_num(np.abs(got_o - want_o), nan=np.inf).max()), \
+        float(np.nan_to_num(np.abs(got_l - want_l), nan=np.inf).max())
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("cuts", [(0, 37), (0, 5, 16, 30, 37), (0, 1, 2, 3, 37), (0, 36, 37), (0, 12, 24, 48)])
+@pytest.mark.parametrize("scale", [0.3, 40.0])
+def test_merge_of_partials_is_full_attention(causal, cuts, scale):
+    """Any partition of the keys (empty and single-key runs, runs past Sk) merges back exactly,
+    also with logits large enough that exp(LSE) overflows float32 (scale 40)."""
+    d_o, d_l = _partition_check(merge_partials, causal=causal, cuts=cuts, scale=scale)
+    assert d_o < 1e-5 and d_l < 2e-6 * max(1.0, scale)  # float32 rounding of both sides
+
+
+def test_partial_matches_bruteforce_on_a_range():
+    rng = np.random.default_rng(9)
+    q, k, v = (rng.standard_normal((9, 8)).astype(np.float32) for _ in range(3))
+    o, l = attention_partial(q, k, v, True, 0.5, 3, 7)
+    for i in range(9):
+        keys = [j for j in range(3, 7) if j <= i]
+        if not keys:
+            assert l[i] == -np.inf and not o[i].any()
+            continue
+        s = np.array([0.5 * float(q[i] @ k[j]) for j in keys], dtype=np.float64)
+        lse = s.max() + math.log(np.exp(s - s.max()).sum())
+        want = sum(math.exp(sj - lse) * v[j].astype(np.float64) for sj, j in zip(s, keys))
+        assert abs(l[i] - lse) < 1e-5 and np.abs(o[i] - want).max() < 1e-5
+
+
+def _merge_mutant_unweighted(parts):   # plain average of the partial outputs
+    o = np.mean([p[0] for p in parts], axis=0)
+    return o.astype(np.float32), merge_partials(parts)[1]
+
+
+def _merge_mutant_no_max(parts):       # weights exp(LSE_s) without the max shift: overflows in float32
+    lses = np.stack([p[1] for p in parts]).astype(np.float32)
+    w = np.exp(lses)
+    lse = np.log(w.sum(axis=0))
+    o = (w[..., None] * np.stack([p[0] for p in parts])).sum(axis=0) / w.sum(axis=0)[..., None]
+    return o.astype(np.float32), lse.astype(np.float32)
+
+
+def _merge_mutant_base2(parts):        # weights in base 2
+    lses = np.stack([p[1] for p in parts]).astype(np.float64)
+    m = lses.max(axis=0)
+    w = np.where(np.isfinite(lses), np.exp2(lses - m), 0.0)
+    o = (w[..., None] * np.stack([p[0] for p in parts])).sum(axis=0) / w.sum(axis=0)[..., None]
+    return o.astype(np.float32), (m + np.log(w.sum(axis=0))).astype(np.float32)
+
+
+@pytest.mark.parametrize("mutant", [_merge_mutant_unweighted, _merge_mutant_no_max, _merge_mutant_base2],
+                         ids=["unweighted", "no_max", "base2"])
+def test_partition_identity_rejects_merge_mutants(mutant):
+    results = [_partition_check(mutant, causal=True, cuts=(0, 5, 16, 30, 37), scale=sc) for sc in (0.3, 40.0)]
+    assert any(d_o > 1e-3 or d_l > 1e-3 for d_o, d_l in results)
