@@ -1702,25 +1702,16 @@ int launch(const fa_fwd_params *p, void *hip_stream, int splits, void *workspace
     if (nq > plan.grid) nq = plan.grid;
     if (nq > bh) nq = bh;
     a.nq = (int32_t)nq;
-    // Queue order: all of a queue's heads at once (heaviest first across
-    // them) while their K+V fit in 16 MiB of L2 + MALL reuse distance;
-    // otherwise groups small enough for that, but at least large enough that
-    // a group has ~4 tiles per worker, in two weight bands.  Measured on the
-    // five benchmark workloads (within 1-3% of the best fixed choice each).
+    // Queue order: a queue's heads in groups of 8, each group's tiles
+    // heaviest first across its heads, one band.  Measured on the benchmark
+    // workloads against groups of 2..64 heads and 1..4 bands: within 1% of
+    // the best time on each, with the least HBM traffic or close to it
+    // (e.g. B8 H32 S3000 causal: 646 us and 2.5 GB fetched per launch, against
+    // 804 us and 6.6 GB for all 32 heads of a queue at once; B16 H16 S1024:
+    // 87 us against 101 us).
     const int64_t nh = (bh + nq - 1) / nq;  // heads of queue 0
-    const int64_t workers = plan.grid / nq;
-    const int64_t kv_head = (int64_t)p->Sk * p->D * 2 * 2;
-    const int64_t budget = (int64_t)16 << 20;
-    int64_t group = nh;
-    if (nh * kv_head > budget) {
-      const int64_t by_l2 = budget / kv_head > 1 ? budget / kv_head : 1;
-      const int64_t by_work = (4 * workers + plan.n_mtiles - 1) / plan.n_mtiles;
-      group = by_l2 > by_work ? by_l2 : by_work;
-      if (group > nh) group = nh;
-      if (group > by_l2 && by_l2 * 2 >= by_work) group = by_l2;
-    }
-    a.q_group = (int32_t)(group > 0 ? group : 1);
-    a.q_bands = 2;
+    a.q_group = (int32_t)(nh < 8 ? (nh > 0 ? nh : 1) : 8);
+    a.q_bands = 1;
   }
   // A negative scale is folded into Q (sign flip of every element, exact),
   // a zero scale into a tiny positive one (all logits ~0: uniform weights).

@@ -171,6 +171,9 @@ def run_passes(out: Path, target: list[str], plan=None, timeout=120) -> dict:
     plan = METRIC_PLAN if plan is None else plan
     out = Path(out).resolve()
     out.mkdir(parents=True, exist_ok=True)
+    # The passes run from /tmp: make the command's relative file arguments
+    # (e.g. `python3 bench.py`) absolute first.
+    target = [str(Path(a).resolve()) if not a.startswith("-") and Path(a).is_file() else a for a in target]
     # The passes run from /tmp (rocprofv3 writes scratch files there); keep
     # this repository importable for a `python -m flash_attn_npu_amd...` target.
     repo = str(Path(__file__).resolve().parent.parent)
