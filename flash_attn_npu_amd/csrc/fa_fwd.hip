@@ -55,6 +55,7 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -558,12 +559,38 @@ __device__ __forceinline__ int swz(int r) {
   }
 }
 
+// Chunk swizzle of fp8-e5m2 V rows (D bytes), read with ds_read_b64_tr_b8.
+// One read's half-wave touches rows {0..3, 8..11} of a 16-key step (+4 in
+// the upper half-wave), 8 bytes in each of two adjacent chunks per row:
+//  * D = 128 (two rows per 256-byte bank row): the four rows of one parity
+//    get distinct even chunk offsets, 2 ((r >> 1) & 1) + 4 ((r >> 3) & 1);
+//  * D = 64 (four rows per bank row): rows r and r + 8 differ by 2 chunks.
+template <int D>
+__device__ __forceinline__ int swz8(int r) {
+  if constexpr (D == 128) {
+    return (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
+  } else {
+    static_assert(D == 64, "fp8 V head dim");
+    return ((r >> 3) & 1) << 1;
+  }
+}
+
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) char lds_char;
 
 __device__ __forceinline__ u32x2_t lds_read_tr16(const char *smem_base, uint32_t off) {
   const lds_char *p = (const lds_char *)smem_base + off;
   i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t *)p);
+  return __builtin_bit_cast(u32x2_t, v);
+}
+
+// Transposing 8-bit read (ds_read_b64_tr_b8): in each group of 16 lanes,
+// output lane i receives, as byte j of its 8 bytes, byte (i % 8) of the
+// 8 bytes addressed by lane 2j + i/8 of the group.
+__device__ __forceinline__ u32x2_t lds_read_tr8(const char *smem_base, uint32_t off) {
+  const lds_char *p = (const lds_char *)smem_base + off;
+  typedef int i32x2_t __attribute__((ext_vector_type(2)));
+  i32x2_t v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2_t *)p);
   return __builtin_bit_cast(u32x2_t, v);
 }
 
@@ -600,33 +627,47 @@ constexpr int kSchedVmem = 0x010;
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
 
-template <int D, int BN, int NW, int NSTAGE, int OCC>
+template <int D, int BN, int NW, int NSTAGE, int OCC, bool V8 = false>
 struct Cfg2 {
   static constexpr int BM = 32 * NW;
   static constexpr int NT = 64 * NW;
-  static constexpr int ROW = 2 * D;           // bytes per K/V row in LDS
+  static constexpr int ROW = 2 * D;           // bytes per K row in LDS
   static constexpr int CPR = ROW / 16;        // 16-byte chunks per row
   static constexpr int RPI = 1024 / ROW;      // rows per DMA instruction (64 lanes x 16 B)
-  static constexpr int TILE = BN * ROW;       // bytes of one K (or V) tile
-  static constexpr int IPT = TILE / 1024;     // DMA instructions per tile and tensor
+  static constexpr int TILE = BN * ROW;       // bytes of one K tile
+  static constexpr int IPT = TILE / 1024;     // DMA instructions per K tile
   static constexpr int IPW = IPT / NW;        // ... per wave
-  static constexpr int STAGE = 2 * TILE;
+  // V rows: D 16-bit elements, or D bytes when V is fp8-e5m2 (V8).
+  static constexpr int VROW = V8 ? D : 2 * D;
+  static constexpr int VCPR = VROW / 16;
+  static constexpr int VRPI = 1024 / VROW;
+  static constexpr int VTILE = BN * VROW;
+  static constexpr int VIPT = VTILE / 1024;
+  static constexpr int VIPW = VIPT / NW;
+  static constexpr int NDMA = IPW + VIPW;     // DMA instructions per wave and tile
+  static constexpr int STAGE = TILE + VTILE;
   static constexpr int LDS_BYTES = NSTAGE * STAGE;
   // O^T blocks of 32 head dims; D = 16 uses one block whose upper 16 rows
   // come out zero (the V^T operand rows past D are zeroed).
   static constexpr int DB = D >= 32 ? D / 32 : 1;
   static_assert(D == 16 || D == 32 || D == 64 || D == 128 || D == 256, "head dim");
   static_assert(IPT % NW == 0 && IPW >= 1, "DMA instructions must split evenly over waves");
+  static_assert(VIPT % NW == 0 && VIPW >= 1, "DMA instructions must split evenly over waves");
+  static_assert(!V8 || ((D == 64 || D == 128) && BN == 64), "fp8 V: head dim 64 or 128, 64-key tiles");
   static_assert(BN % 32 == 0, "tile shape");
   static_assert(NSTAGE == 2, "double-buffered: one tile computes while the next lands");
   static_assert(OCC == 1 || OCC == 2, "workgroups per CU");
   static_assert(LDS_BYTES * OCC <= 160 * 1024, "LDS budget of one gfx950 CU");
 };
 
-template <int D, int BN, int NW, int NSTAGE, int OCC, bool BF16, bool CAUSAL>
+// V8: V is fp8-e5m2 (reference flash_attention_forward.py:704, :737, :996):
+// P is rounded to e5m2 and O^T += V^T P^T runs on the 32x32x64 fp8 MFMA, one
+// instruction per 32 head dims and 64 keys.  Q, K and O keep their 16-bit type.
+template <int D, int BN, int NW, int NSTAGE, int OCC, bool BF16, bool CAUSAL, bool V8 = false>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OCC * NW / 4, OCC * NW / 4)))
 fa_fwd_dma_kernel(KernelArgs p) {
-  using C = Cfg2<D, BN, NW, NSTAGE, OCC>;
+  using C = Cfg2<D, BN, NW, NSTAGE, OCC, V8>;
+  constexpr int ESV = V8 ? 1 : 2;  // bytes per V element
   constexpr int BM = C::BM;
   // One array per stage: the compiler's LDS-DMA alias tracking then knows
   // that DMAs into one stage never feed reads of the other, and adds no
@@ -643,13 +684,22 @@ fa_fwd_dma_kernel(KernelArgs p) {
   // DMA: instruction j of this wave fills LDS rows (wave + j*NW)*RPI .. +RPI of
   // the tile; lane -> (row, physical chunk), and it fetches the logical chunk
   // that the swizzle stores there.
-  uint32_t dk[C::IPW], dv[C::IPW];
+  uint32_t dk[C::IPW], dv[C::VIPW];
 #pragma unroll
   for (int j = 0; j < C::IPW; ++j) {
     const int row = (wave + j * NW) * C::RPI + lane / C::CPR;
     const int lc = (lane % C::CPR) ^ swz<D>(row);
     dk[j] = (uint32_t)(row * p.k_ss * 2 + lc * 16);
-    dv[j] = (uint32_t)(row * p.v_ss * 2 + lc * 16);
+  }
+#pragma unroll
+  for (int j = 0; j < C::VIPW; ++j) {
+    const int row = (wave + j * NW) * C::VRPI + lane / C::VCPR;
+    int lc = lane % C::VCPR;
+    if constexpr (V8)
+      lc ^= swz8<D>(row);
+    else
+      lc ^= swz<D>(row);
+    dv[j] = (uint32_t)(row * p.v_ss * ESV + lc * 16);
   }
   // K operand reads: lane (h, n) reads key row 32kb + n, logical chunk 2s + h
   // (swz(32kb + n) == swz(n)).
@@ -662,8 +712,24 @@ fa_fwd_dma_kernel(KernelArgs p) {
   // (e, h, j), so one lane offset per (db, e) covers every k-step ks.
   // D = 16: lanes of the upper 16 dims read dims 0..15 again (in range) and
   // their fragments are zeroed before use.
-  uint32_t vro[C::DB][2];
-  {
+  //
+  // fp8 V (8-bit transpose reads, one per 16 keys): the fp8 MFMA pairs byte
+  // j of lane half h of both operands; P^T takes byte j from S^T register
+  // (block j / 16, r = j % 16), i.e. key 16 (j / 8) + 8 ((j % 8) >> 2) + 4h +
+  // (j & 3).  So for the read of key step u (bytes 8u..8u+7), source lane s
+  // of lane group g = lane/16 addresses key row 16u + 8 ((s >> 1) >> 2) +
+  // 4 (g >> 1) + ((s >> 1) & 3), dims 32db + 16 (g & 1) + 8 (s & 1); the
+  // swizzle of that row does not depend on u.
+  uint32_t vro[C::DB][V8 ? 1 : 2];
+  if constexpr (V8) {
+    const int g = lane >> 4, sl = lane & 15, q = sl >> 1;
+    const int row = 8 * (q >> 2) + 4 * (g >> 1) + (q & 3);
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db) {
+      const int lc = 2 * db + (g & 1);
+      vro[db][0] = (uint32_t)(row * C::VROW + ((lc ^ swz8<D>(row)) * 16) + (sl & 1) * 8);
+    }
+  } else {
     const int g = lane >> 4, sg = lane & 15, jj = sg >> 2, cc = sg & 3;
 #pragma unroll
     for (int db = 0; db < C::DB; ++db)
@@ -701,7 +767,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
 
     const char *qg = p.q + 2 * (bb * p.q_sb + hh * p.q_sh);
     const char *kg = p.k + 2 * (bb * p.k_sb + hh * p.k_sh);
-    const char *vg = p.v + 2 * (bb * p.v_sb + hh * p.v_sh);
+    const char *vg = p.v + ESV * (bb * p.v_sb + hh * p.v_sh);
 
     const int kv_end = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
     // KV tiles [t_begin, n_tiles) of this unit: the whole range, or one run
@@ -718,15 +784,23 @@ fa_fwd_dma_kernel(KernelArgs p) {
       const int key0 = t * BN;
       const bool live = t < n_tiles;
       const uint32_t nbk = live ? (uint32_t)((int64_t)(p.Sk - key0) * p.k_ss * 2) : 0u;
-      const uint32_t nbv = live ? (uint32_t)((int64_t)(p.Sk - key0) * p.v_ss * 2) : 0u;
+      const uint32_t nbv = live ? (uint32_t)((int64_t)(p.Sk - key0) * p.v_ss * ESV) : 0u;
       *rk = make_rsrc(kg + (int64_t)key0 * p.k_ss * 2, nbk);
-      *rv = make_rsrc(vg + (int64_t)key0 * p.v_ss * 2, nbv);
+      *rv = make_rsrc(vg + (int64_t)key0 * p.v_ss * ESV, nbv);
     };
+    // With fp8 V the K instructions come first, then the (fewer) V ones.
     auto dma = [&](auto stage_tag, const BufRsrc &rk, const BufRsrc &rv, int i) __attribute__((always_inline)) {
       constexpr int STG = decltype(stage_tag)::value;
       char *base = STG == 0 ? smem0 : smem1;
-      const int j = i >> 1;
-      dma16_lds((i & 1) ? rv : rk, base + (i & 1) * C::TILE + (wave + j * NW) * 1024, (i & 1) ? dv[j] : dk[j]);
+      if constexpr (V8) {
+        if (i < C::IPW)
+          dma16_lds(rk, base + (wave + i * NW) * 1024, dk[i]);
+        else
+          dma16_lds(rv, base + C::TILE + (wave + (i - C::IPW) * NW) * 1024, dv[i - C::IPW]);
+      } else {
+        const int j = i >> 1;
+        dma16_lds((i & 1) ? rv : rk, base + (i & 1) * C::TILE + (wave + j * NW) * 1024, (i & 1) ? dv[j] : dk[j]);
+      }
     };
 
     // Prologue: KV tile t_begin into its stage (t_begin & 1).
@@ -735,10 +809,10 @@ fa_fwd_dma_kernel(KernelArgs p) {
       tile_rsrc(t_begin, &rk, &rv);
       if (t_begin & 1) {
 #pragma unroll
-        for (int i = 0; i < 2 * C::IPW; ++i) dma(std::integral_constant<int, 1>{}, rk, rv, i);
+        for (int i = 0; i < C::NDMA; ++i) dma(std::integral_constant<int, 1>{}, rk, rv, i);
       } else {
 #pragma unroll
-        for (int i = 0; i < 2 * C::IPW; ++i) dma(std::integral_constant<int, 0>{}, rk, rv, i);
+        for (int i = 0; i < C::NDMA; ++i) dma(std::integral_constant<int, 0>{}, rk, rv, i);
       }
     }
 
@@ -782,7 +856,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
       // The next tile's DMAs go into the other stage (free after the
       // barrier); they are spread over the QK MFMAs below, or issued here
       // when this wave has no work in this tile.
-      constexpr int NDMA = 2 * C::IPW;
+      constexpr int NDMA = C::NDMA;
       using NEXT = std::integral_constant<int, 1 - STG>;
       BufRsrc rk_n, rv_n;
       tile_rsrc(t + 1, &rk_n, &rv_n);
@@ -816,8 +890,20 @@ fa_fwd_dma_kernel(KernelArgs p) {
       // reads so they land during the softmax.
       constexpr int NQK = (D / 16) * (BN / 32);
       constexpr int KPF = 4;
-      constexpr int NPV = (BN / 16) * C::DB;
-      constexpr int VPF = 2;
+      constexpr int NPV = V8 ? C::DB : (BN / 16) * C::DB;
+      constexpr int VPF = V8 ? 1 : 2;
+      constexpr int VRD = V8 ? 4 : 2;  // LDS reads per V^T fragment
+      // fp8 V^T fragment of head dims 32db.. for all 64 keys (32 bytes per lane).
+      auto vread8 = [&](int db) {
+        i32x8_t f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const u32x2_t x = lds_read_tr8(sbase, vro[db][0] + (uint32_t)(C::TILE + 16 * u * C::VROW));
+          f[2 * u] = (int)x[0];
+          f[2 * u + 1] = (int)x[1];
+        }
+        return f;
+      };
       auto vread = [&](int i) {
         const int ks = i / C::DB, db = i % C::DB;
         const uint32_t imm = (uint32_t)(C::TILE + 16 * ks * C::ROW);
@@ -830,7 +916,8 @@ fa_fwd_dma_kernel(KernelArgs p) {
         return f;
       };
       u32x4_t kfr[NQK];
-      u32x4_t vfr[NPV];
+      u32x4_t vfr[V8 ? 1 : NPV];
+      i32x8_t vfr8[V8 ? NPV : 1];
       f32x16_t sacc[BN / 32];
 #pragma unroll
       for (int kb = 0; kb < BN / 32; ++kb) sacc[kb] = (f32x16_t){};
@@ -848,7 +935,12 @@ fa_fwd_dma_kernel(KernelArgs p) {
         if (i + KPF < NQK) kfr[i + KPF] = kread(i + KPF);
         if (i + KPF == NQK) {
 #pragma unroll
-          for (int j = 0; j < VPF; ++j) vfr[j] = vread(j);
+          for (int j = 0; j < VPF; ++j) {
+            if constexpr (V8)
+              vfr8[j] = vread8(j);
+            else
+              vfr[j] = vread(j);
+          }
         }
         const int s = i / (BN / 32), kb = i % (BN / 32);
         sacc[kb] = mfma32x32x16<BF16>(kfr[i], qf[s], sacc[kb]);
@@ -860,7 +952,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
         if (i < NDMA) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
         if (i + KPF < NQK) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-        if (i + KPF == NQK) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * VPF, 0);
+        if (i + KPF == NQK) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, VRD * VPF, 0);
       }
 
       if (MASKED) {
@@ -905,6 +997,31 @@ fa_fwd_dma_kernel(KernelArgs p) {
           lsum[r & 3] = (kb == 0 && r < 4) ? pv : lsum[r & 3] + pv;
         }
 
+      if constexpr (V8) {
+        // P^T in e5m2 (round to nearest even): byte j = register j % 16 of
+        // block j / 16, four bytes per VGPR.
+        i32x8_t pf8;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+          const int kb = w >> 2, r0 = 4 * (w & 3);
+          const int lo = __builtin_amdgcn_cvt_pk_bf8_f32(sacc[kb][r0], sacc[kb][r0 + 1], 0, false);
+          pf8[w] = __builtin_amdgcn_cvt_pk_bf8_f32(sacc[kb][r0 + 2], sacc[kb][r0 + 3], lo, true);
+        }
+        l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+        // O^T += V^T P^T: one fp8 MFMA per 32 head dims (unit scales: E8M0
+        // exponent 127 = 2^0), the next fragment's four reads ahead of it.
+#pragma unroll
+        for (int db = 0; db < NPV; ++db) {
+          if (db + VPF < NPV) vfr8[db + VPF] = vread8(db + VPF);
+          oacc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vfr8[db], pf8, oacc[db], 1, 1, 0, 127, 0, 127);
+        }
+#pragma unroll
+        for (int i = 0; i < NPV - VPF; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, VRD, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, VPF, 0);
+      } else {
       // P^T fragments: k-step ks (16 keys) = registers 8t..8t+7 of block ks/2.
       u32x4_t pf[BN / 16];
 #pragma unroll
@@ -929,6 +1046,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
       }
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, VPF, 0);
+      }
     };
 
     // Tiles visible to every query of the workgroup need no mask.  Each run
@@ -1511,11 +1629,11 @@ constexpr KernelEntry entry() {
                      fa_fwd_kernel<D, BN, NW, BF16, CAUSAL>};
 }
 
-template <int D, int BN, int NW, int NSTAGE, int OCC, bool BF16, bool CAUSAL>
+template <int D, int BN, int NW, int NSTAGE, int OCC, bool BF16, bool CAUSAL, bool V8 = false>
 constexpr KernelEntry entry_dma() {
-  return KernelEntry{D, BF16 ? 1 : 0, CAUSAL ? 1 : 0, BN, NW, NSTAGE,
-                     Cfg2<D, BN, NW, NSTAGE, OCC>::LDS_BYTES, OCC, true,
-                     fa_fwd_dma_kernel<D, BN, NW, NSTAGE, OCC, BF16, CAUSAL>};
+  return KernelEntry{D, (BF16 ? FA_DTYPE_BF16 : FA_DTYPE_FP16) + (V8 ? 2 : 0), CAUSAL ? 1 : 0, BN, NW, NSTAGE,
+                     Cfg2<D, BN, NW, NSTAGE, OCC, V8>::LDS_BYTES, OCC, true,
+                     fa_fwd_dma_kernel<D, BN, NW, NSTAGE, OCC, BF16, CAUSAL, V8>};
 }
 
 #define FA_ENTRIES_DT_C(D, BN, NW)                                                   \
@@ -1529,6 +1647,11 @@ constexpr KernelEntry entry_dma() {
 #define FA_DMA_ENTRIES(D, BN, NW, ST, OCC)                                                     \
   entry_dma<D, BN, NW, ST, OCC, false, false>(), entry_dma<D, BN, NW, ST, OCC, false, true>(), \
       entry_dma<D, BN, NW, ST, OCC, true, false>(), entry_dma<D, BN, NW, ST, OCC, true, true>()
+
+// fp8-e5m2 V with fp16 / bf16 Q, K, O (dtype codes FA_DTYPE_*_V_E5M2).
+#define FA_DMA8_ENTRIES(D, BN, NW, ST, OCC)                                                                  \
+  entry_dma<D, BN, NW, ST, OCC, false, false, true>(), entry_dma<D, BN, NW, ST, OCC, false, true, true>(), \
+      entry_dma<D, BN, NW, ST, OCC, true, false, true>(), entry_dma<D, BN, NW, ST, OCC, true, true, true>()
 
 // The first entry matching (D, dtype, causal, BLOCK_N, waves) serves a launch.
 const KernelEntry kKernels[] = {
@@ -1544,12 +1667,22 @@ const KernelEntry kKernels[] = {
     FA_DMA_ENTRIES(32, 64, 4, 2, 2),
     // D = 16: a 64-key tile is only two DMA instructions; 128 keys give each wave one.
     FA_DMA_ENTRIES(16, 128, 4, 2, 2),
+    FA_DMA8_ENTRIES(128, 64, 4, 2, 2),
+    FA_DMA8_ENTRIES(64, 64, 4, 2, 2),
     FA_ENTRIES_DT_C(64, 64, 4),
     FA_ENTRIES_DT_C(128, 64, 4),
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
 bool is_supported_head_dim(int d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
+
+bool is_valid_dtype(int dt) {
+  return dt == FA_DTYPE_FP16 || dt == FA_DTYPE_BF16 || dt == FA_DTYPE_FP16_V_E5M2 || dt == FA_DTYPE_BF16_V_E5M2;
+}
+bool v_is_fp8(int dt) { return dt == FA_DTYPE_FP16_V_E5M2 || dt == FA_DTYPE_BF16_V_E5M2; }
+bool out_is_bf16(int dt) { return dt == FA_DTYPE_BF16 || dt == FA_DTYPE_BF16_V_E5M2; }
+// Head dims of the fp8-V kernels.
+bool is_supported_fp8v_head_dim(int d) { return d == 64 || d == 128; }
 
 // Default (BLOCK_N, waves) per head dim; BLOCK_M = 32 * waves.
 void default_tiling(int D, int dtype, int causal, int *bn, int *nw) {
@@ -1735,7 +1868,7 @@ int launch(const fa_fwd_params *p, void *hip_stream, int splits, void *workspace
     m.B = p->B; m.H = p->H; m.Sq = p->Sq; m.D = p->D; m.splits = splits;
     const int64_t rows = (int64_t)p->B * p->H * p->Sq;
     const unsigned blocks = (unsigned)((rows + 3) / 4);
-    if (p->dtype == FA_DTYPE_BF16) {
+    if (out_is_bf16(p->dtype)) {
       hipLaunchKernelGGL(fa_merge_kernel<true>, dim3(blocks), dim3(256), 0, stream, m);
     } else {
       hipLaunchKernelGGL(fa_merge_kernel<false>, dim3(blocks), dim3(256), 0, stream, m);
@@ -1757,8 +1890,8 @@ const char *fa_error_string(int code) {
     case FA_ERR_NULL: return "a required tensor pointer is NULL";
     case FA_ERR_SHAPE: return "invalid shape (negative size, Sq>0 with Sk==0, or too many tiles)";
     case FA_ERR_HEAD_DIM: return "HEAD_DIM is not supported by this build";
-    case FA_ERR_DTYPE: return "dtype must be fp16 or bf16";
-    case FA_ERR_STRIDE: return "the head-dim stride must be 1 and the other strides multiples of 8 elements";
+    case FA_ERR_DTYPE: return "dtype must be fp16 or bf16 (optionally with fp8-e5m2 V)";
+    case FA_ERR_STRIDE: return "the head-dim stride must be 1 and the other strides multiples of 8 elements (16 for an fp8 V)";
     case FA_ERR_ALIGN: return "tensor base pointers must be 16-byte aligned";
     case FA_ERR_TILING: return "unsupported BLOCK_M/BLOCK_N combination";
     case FA_ERR_SCALE: return "sm_scale must be finite";
@@ -1773,7 +1906,8 @@ int fa_validate(const fa_fwd_params *p) {
   if (p->B < 0 || p->H < 0 || p->Sq < 0 || p->Sk < 0 || p->D <= 0) return FA_ERR_SHAPE;
   if (p->Sq > 0 && p->Sk == 0 && p->B > 0 && p->H > 0) return FA_ERR_SHAPE;
   if (!is_supported_head_dim(p->D)) return FA_ERR_HEAD_DIM;
-  if (p->dtype != FA_DTYPE_FP16 && p->dtype != FA_DTYPE_BF16) return FA_ERR_DTYPE;
+  if (!is_valid_dtype(p->dtype)) return FA_ERR_DTYPE;
+  if (v_is_fp8(p->dtype) && !is_supported_fp8v_head_dim(p->D)) return FA_ERR_HEAD_DIM;
   if (!(p->sm_scale == p->sm_scale) || isinf(p->sm_scale)) return FA_ERR_SCALE;
   if (p->num_programs < 0) return FA_ERR_GRID;
   if ((p->block_m == 0) != (p->block_n == 0)) return FA_ERR_TILING;
@@ -1783,9 +1917,11 @@ int fa_validate(const fa_fwd_params *p) {
   const int64_t *st[4] = {p->q_stride, p->k_stride, p->v_stride, p->o_stride};
   const int64_t rows[4] = {p->Sq, p->Sk, p->Sk, p->Sq};
   for (int t = 0; t < 4; ++t) {
+    // 16-byte rows: strides in multiples of 8 16-bit or 16 fp8 elements.
+    const int64_t align = (t == 2 && v_is_fp8(p->dtype)) ? 16 : 8;
     if (st[t][3] != 1) return FA_ERR_STRIDE;
     for (int i = 0; i < 3; ++i)
-      if (st[t][i] < 0 || st[t][i] % 8 != 0) return FA_ERR_STRIDE;
+      if (st[t][i] < 0 || st[t][i] % align != 0) return FA_ERR_STRIDE;
     if (rows[t] > 1 && st[t][2] < p->D) return FA_ERR_STRIDE;
     // Buffer offsets inside one (b, h) slice are 32-bit: keep the slice, plus
     // the rows past its end that a last partial m-tile or the DMAs issued past
@@ -1804,7 +1940,8 @@ int fa_query_config(const fa_fwd_params *p, int32_t out[FA_CFG_COUNT]) {
   if (p == nullptr || out == nullptr) return FA_ERR_NULL;
   if (p->B < 0 || p->H < 0 || p->Sq < 0 || p->Sk < 0) return FA_ERR_SHAPE;
   if (!is_supported_head_dim(p->D)) return FA_ERR_HEAD_DIM;
-  if (p->dtype != FA_DTYPE_FP16 && p->dtype != FA_DTYPE_BF16) return FA_ERR_DTYPE;
+  if (!is_valid_dtype(p->dtype)) return FA_ERR_DTYPE;
+  if (v_is_fp8(p->dtype) && !is_supported_fp8v_head_dim(p->D)) return FA_ERR_HEAD_DIM;
   if ((p->block_m == 0) != (p->block_n == 0)) return FA_ERR_TILING;
   if (p->num_programs < 0) return FA_ERR_GRID;
   Plan plan;
@@ -1856,7 +1993,7 @@ int fa_fwd_split(const fa_fwd_params *p, int32_t kv_splits, void *workspace, int
 int32_t fa_default_kv_splits(const fa_fwd_params *p) {
   // Shape-only (no pointer or stride checks): usable before tensors exist.
   if (p == nullptr || p->B <= 0 || p->H <= 0 || p->Sq <= 0 || p->Sk <= 0) return 1;
-  if (!is_supported_head_dim(p->D) || (p->dtype != FA_DTYPE_FP16 && p->dtype != FA_DTYPE_BF16)) return 1;
+  if (!is_supported_head_dim(p->D) || !is_valid_dtype(p->dtype)) return 1;
   Plan plan;
   if (make_plan(p, &plan) != FA_OK) return 1;
   const KernelEntry &e = kKernels[plan.kernel];

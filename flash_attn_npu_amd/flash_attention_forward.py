@@ -67,6 +67,13 @@ FA_ERR_LAUNCH = -100
 _ARGUMENT_ERRORS = {-1, -2, -3, -4, -5, -6, -7, -8, -9}
 FA_CFG_COUNT = 8
 FA_DTYPE = {torch.float16: 0, torch.bfloat16: 1}
+# fp8-e5m2 V with fp16 / bf16 q, k, o: dtype code + FA_DTYPE_V_E5M2_OFFSET
+# (FA_DTYPE_FP16_V_E5M2 = 2, FA_DTYPE_BF16_V_E5M2 = 3).
+FP8_V_DTYPE = torch.float8_e5m2
+FA_DTYPE_V_E5M2_OFFSET = 2
+FP8_V_HEAD_DIMS = (64, 128)
+FP8_V_TILING = (128, 64)
+_DTYPE_NAMES = {0: "float16", 1: "bfloat16", 2: "float16+float8_e5m2_v", 3: "bfloat16+float8_e5m2_v"}
 
 
 class FaFwdParams(ctypes.Structure):
@@ -164,7 +171,7 @@ def kernel_table():
     rows = []
     for i in range(lib.fa_num_kernels()):
         _check(lib.fa_kernel_info(i, out), "fa_kernel_info")
-        rows.append({"HEAD_DIM": out[0], "dtype": "bfloat16" if out[1] else "float16",
+        rows.append({"HEAD_DIM": out[0], "dtype": _DTYPE_NAMES.get(out[1], str(out[1])),
                      "causal": bool(out[2]), "BLOCK_M": out[3], "BLOCK_N": out[4], "waves": out[5]})
     return rows
 
@@ -281,16 +288,19 @@ def _validate_inputs(q, k, v):
     if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
         raise ValueError(f"HEAD_DIM={q.shape[-1]} is not supported by this build "
                          f"(supported: {SUPPORTED_HEAD_DIMS})")
-    if q.dtype not in FA_DTYPE or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise ValueError("q, k, v must all be float16 or all be bfloat16")
+    if q.dtype not in FA_DTYPE or k.dtype != q.dtype or (v.dtype != q.dtype and v.dtype != FP8_V_DTYPE):
+        raise ValueError("q, k, v must all be float16 or all be bfloat16 (v may also be float8_e5m2)")
+    if v.dtype == FP8_V_DTYPE and q.shape[-1] not in FP8_V_HEAD_DIMS:
+        raise ValueError(f"a float8_e5m2 v is supported for HEAD_DIM in {FP8_V_HEAD_DIMS}")
     if q.device.type != "cuda":
         raise ValueError(f"q, k, v must be GPU tensors (device 'cuda'), got {q.device}")
 
 
 def _kernel_ready(t):
-    """A view the kernel can read directly: dim stride 1, other strides %8, 16B-aligned."""
+    """A view the kernel can read directly: dim stride 1, 16-byte rows, 16B-aligned."""
     st = t.stride()
-    if st[3] != 1 or any(s % 8 for s in st[:3]) or t.data_ptr() % 16:
+    align = 16 // t.element_size()
+    if st[3] != 1 or any(s % align for s in st[:3]) or t.data_ptr() % 16:
         return t.contiguous()
     if t.shape[2] > 1 and st[2] < t.shape[3]:
         return t.contiguous()
@@ -309,7 +319,10 @@ def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
     """
     _validate_inputs(q, k, v)
     z, h, n_ctx, head_dim = q.shape
-    bm, bn, _ = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn)
+    fp8_v = v.dtype == FP8_V_DTYPE
+    bm, bn, source = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn)
+    if fp8_v and source != "override":
+        bm, bn = FP8_V_TILING  # the fp8-V kernels' one tiling; presets are for 16-bit V
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     out = torch.empty_like(q)
     lse = torch.empty((z, h, n_ctx), device=q.device, dtype=torch.float32)
@@ -328,7 +341,7 @@ def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
     _fill_strides(p.v_stride, v)
     _fill_strides(p.o_stride, out)
     p.B, p.H, p.Sq, p.Sk, p.D = z, h, n_ctx, n_ctx, head_dim
-    p.dtype = FA_DTYPE[q.dtype]
+    p.dtype = FA_DTYPE[q.dtype] + (FA_DTYPE_V_E5M2_OFFSET if fp8_v else 0)
     p.causal = 1 if causal else 0
     p.sm_scale = sm_scale
     p.block_m, p.block_n = int(bm), int(bn)

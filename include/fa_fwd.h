@@ -18,7 +18,9 @@
  *    elements, the seq stride at least D when the sequence has more than one
  *    row, and the base pointers 16-byte aligned (128-bit loads and stores).
  *    One (batch, head) slice of a tensor must span less than 2 GiB.
- *  - q, k, v and o share one element type: fp16 or bf16.  lse is fp32,
+ *  - q, k and o share one element type, fp16 or bf16; v has that type too,
+ *    or is fp8-e5m2 (FA_DTYPE_*_V_E5M2, head dims 64 and 128; v strides then
+ *    multiples of 16 elements).  lse is fp32,
  *    contiguous [B, H, Sq], natural log, over the scaled logits
  *    (lse[i] = log(sum_j exp(sm_scale * q_i . k_j)) over the visible keys),
  *    matching the reference's `m_i += log(l_i)` store at
@@ -42,6 +44,11 @@ extern "C" {
 enum fa_dtype {
   FA_DTYPE_FP16 = 0,
   FA_DTYPE_BF16 = 1,
+  /* v is fp8-e5m2 (OCP), q/k/o fp16 or bf16: P is rounded to e5m2 before
+   * P.V, as the reference does when V.dtype is float8e5
+   * (flash_attention_forward.py:704, :737, :996). */
+  FA_DTYPE_FP16_V_E5M2 = 2,
+  FA_DTYPE_BF16_V_E5M2 = 3,
 };
 
 enum fa_status {
@@ -49,7 +56,7 @@ enum fa_status {
   FA_ERR_NULL = -1,        /* a required pointer is NULL                         */
   FA_ERR_SHAPE = -2,       /* negative size, Sq>0 with Sk==0, size overflow       */
   FA_ERR_HEAD_DIM = -3,    /* head dim not in the supported set                   */
-  FA_ERR_DTYPE = -4,       /* dtype is not fp16/bf16                              */
+  FA_ERR_DTYPE = -4,       /* dtype is not an enum fa_dtype value                 */
   FA_ERR_STRIDE = -5,      /* dim stride != 1 or a stride not a multiple of 8     */
   FA_ERR_ALIGN = -6,       /* a base pointer is not 16-byte aligned               */
   FA_ERR_TILING = -7,      /* block_m/block_n/num_waves: unsupported combination  */
@@ -72,7 +79,7 @@ typedef struct fa_fwd_params {
   int64_t v_stride[4];
   int64_t o_stride[4];
   int32_t B, H, Sq, Sk, D;    /* the reference requires Sq == Sk; the kernel does not */
-  int32_t dtype;              /* enum fa_dtype; o has the same type as q/k/v */
+  int32_t dtype;              /* enum fa_dtype; o has the type of q and k */
   int32_t causal;             /* 0 or 1 */
   float sm_scale;
   int32_t block_m;            /* 0 = library default for (D, dtype, causal, S) */

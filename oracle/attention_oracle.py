@@ -35,6 +35,24 @@ with m = max_s LSE_s.  They are pinned by the partition identity: merging the
 partials of any partition of the keys reproduces attention_ref
 (tests/test_oracle.py, including mutants of the merge).
 
+`attention_fp8v` restates the reference's fp8-e5m2 V path
+(flash_attention_forward.py:704, :737, :996): when V is float8e5, the
+unnormalised probabilities of each KV tile, p = exp(s - m) against the running
+row max m, are cast to e5m2 (`p.to(tl.float8e5)`) before `tl.dot(p, v)`,
+while the row sum l accumulates the unrounded fp32 p.  Where the cast falls
+depends on the tile size and on when m moves, so the function replays one
+schedule, given by `block_n` and `lazy_threshold`: tiles of block_n keys from
+key 0, exp2 of (s * c - m) with c = |sm_scale| * log2(e) in fp32, and m moved
+only when a tile's max exceeds it by more than lazy_threshold (in log2 units;
+0 is the reference's always-move rule).  `round_e5m2` is the OCP e5m2 format
+(1 sign, 5 exponent bits with bias 15, 2 mantissa bits, subnormals in steps
+of 2^-16, no saturation) with round-to-nearest-even.  Pinning: round_e5m2
+against known values from the format definition and against torch's
+float8_e5m2 cast; attention_fp8v with the cast disabled against
+attention_ref (online softmax = softmax, any block_n / threshold); with the
+cast, against attention_ref within the e5m2 error bound
+|O - O_ref| <= 2^-3 * sum_j (p_j / l) |v_j|, and an unchanged LSE.
+
 Rounding helpers produce the fp16 / bf16 values the GPU path writes, so that
 an output can be compared to the oracle after the same final cast the
 reference applies (`.to(q.dtype)`, evaluate_attention.py:143).
@@ -62,8 +80,13 @@ __all__ = [
     "round_bf16",
     "round_fp16",
     "round_to",
+    "round_e5m2",
+    "attention_fp8v",
     "attention_flops",
 ]
+
+LOG2E = 1.4426950408889634
+LN2 = 0.6931471805599453
 
 
 def round_bf16(x: np.ndarray) -> np.ndarray:
@@ -90,6 +113,85 @@ def round_to(x: np.ndarray, dtype: str | None) -> np.ndarray:
     if dtype in ("float16", "fp16"):
         return round_fp16(x)
     raise ValueError(f"unsupported dtype {dtype!r}")
+
+
+def round_e5m2(x: np.ndarray) -> np.ndarray:
+    """float32 -> nearest OCP fp8-e5m2 value, returned as float32.
+
+    In the binade [2^e, 2^(e+1)) with e >= -14 the e5m2 values are spaced
+    2^(e-2); below 2^-14 (subnormals) they are spaced 2^-16.  Ties go to the
+    even neighbour; magnitudes that round to 2^16 or beyond (from 61440 =
+    (57344 + 65536) / 2 up) become inf, as the cast does without saturation.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    ax = np.abs(x).astype(np.float64)
+    finite = np.isfinite(ax)
+    _, ex = np.frexp(np.where(finite & (ax > 0), ax, 1.0))  # ax = m 2^ex, m in [0.5, 1)
+    e = np.maximum(ex.astype(np.float64) - 1.0, -14.0)
+    quantum = np.exp2(e - 2.0)
+    r = np.rint(np.where(finite, ax, 0.0) / quantum) * quantum  # rint: half to even
+    r = np.where(r >= 65536.0, np.inf, r)
+    out = np.copysign(r, x.astype(np.float64)).astype(np.float32)
+    return np.where(finite, out, x)
+
+
+def attention_fp8v(q, k, v8, causal: bool, sm_scale: float, out_dtype: str | None = None,
+                   block_n: int = 64, lazy_threshold: float = 8.0, round_p: bool = True):
+    """fp8-e5m2 V attention, replaying a tiled online-softmax schedule.
+
+    q, k: [..., S, D] float32 values of the fp16/bf16 inputs; v8: [..., Sk, D]
+    float32 values of the e5m2 V.  For each tile of block_n keys (from key 0):
+    m_cand = fp32(max(s) * c); the row max moves to m_cand only when
+    m_cand > m + lazy_threshold (O and l are then rescaled by 2^(m - m_new));
+    p = 2^(s * c - m) in fp32 (m taken as 0 while no key was seen);
+    l += sum(p); O += e5m2(p) @ v  (round_p=False skips the cast).
+    Returns (out rounded to out_dtype, lse) like attention_ref.
+    """
+    q = np.asarray(q, dtype=np.float32)
+    k = np.asarray(k, dtype=np.float32)
+    v8 = np.asarray(v8, dtype=np.float32)
+    lead = q.shape[:-2]
+    sq, d = q.shape[-2:]
+    sk = k.shape[-2]
+    qf = q.reshape(-1, sq, d)
+    kf = k.reshape(-1, sk, d)
+    vf = v8.reshape(-1, sk, v8.shape[-1]).astype(np.float64)
+    c = np.float32(np.float32(abs(sm_scale)) * np.float32(LOG2E))
+    thr = np.float32(lazy_threshold)
+    out = np.empty((qf.shape[0], sq, vf.shape[-1]), dtype=np.float32)
+    lse = np.empty((qf.shape[0], sq), dtype=np.float32)
+    rows = np.arange(sq)[:, None]
+    for i in range(qf.shape[0]):
+        qi = qf[i] if sm_scale >= 0 else -qf[i]
+        s_all = (qi.astype(np.float64) @ kf[i].astype(np.float64).T).astype(np.float32)
+        m = np.full(sq, -np.inf, dtype=np.float32)
+        l = np.zeros(sq, dtype=np.float32)
+        acc = np.zeros((sq, vf.shape[-1]), dtype=np.float64)
+        for lo in range(0, sk, block_n):
+            hi = min(lo + block_n, sk)
+            st = s_all[:, lo:hi]
+            if causal:
+                st = np.where(np.arange(lo, hi)[None, :] > rows, np.float32(-np.inf), st)
+            m_cand = (st.max(axis=1) * c).astype(np.float32)
+            upd = m_cand > (m + thr)
+            m_new = np.where(upd, m_cand, m)
+            with np.errstate(invalid="ignore"):
+                alpha = np.where(upd, np.exp2((m - m_new).astype(np.float32)), np.float32(1.0)).astype(np.float32)
+            l = (l * alpha).astype(np.float32)
+            acc *= alpha[:, None].astype(np.float64)
+            m = m_new
+            mb = np.where(m == -np.inf, np.float32(0.0), m)
+            x = (st.astype(np.float64) * np.float64(c) - mb[:, None].astype(np.float64)).astype(np.float32)
+            p = np.exp2(x).astype(np.float32)
+            l = (l + p.sum(axis=1, dtype=np.float32)).astype(np.float32)
+            pr = round_e5m2(p) if round_p else p
+            acc += pr.astype(np.float64) @ vf[i, lo:hi]
+        out[i] = (acc * (1.0 / l.astype(np.float64))[:, None]).astype(np.float32)
+        with np.errstate(divide="ignore"):
+            lse[i] = ((m + np.log2(l)) * np.float32(LN2)).astype(np.float32)
+    out = out.reshape(*lead, sq, vf.shape[-1])
+    lse = lse.reshape(*lead, sq)
+    return round_to(out, out_dtype), lse
 
 
 def _causal_mask(sq: int, sk: int) -> np.ndarray:

@@ -106,6 +106,25 @@ def test_validate_rejects(lib, mutate, code):
     assert lib.fa_error_string(code) != b"unknown fa_fwd status"
 
 
+def test_validate_fp8_v(lib):
+    # dtype 2 / 3: fp16 / bf16 q, k, o with an fp8-e5m2 v (head dims 64 and 128).
+    for dt in (2, 3):
+        for d in (64, 128):
+            assert lib.fa_validate(ctypes.byref(_params(shape=(1, 2, 128, d), dtype=dt))) == 0, (dt, d)
+        for d in (16, 32, 256):
+            assert lib.fa_validate(ctypes.byref(_params(shape=(1, 2, 128, d), dtype=dt))) == -3, (dt, d)
+    # 16-byte rows: an fp8 v needs strides in multiples of 16 elements.
+    p = _params(shape=(1, 2, 128, 64), dtype=3)
+    p.v_stride[2] = 72
+    assert lib.fa_validate(ctypes.byref(p)) == -5
+    p.dtype = 1
+    assert lib.fa_validate(ctypes.byref(p)) == 0
+    out = (ctypes.c_int32 * 8)()
+    assert lib.fa_query_config(ctypes.byref(_params(shape=(4, 32, 2048, 128), dtype=3)), out) == 0
+    assert (out[0], out[1]) == (128, 64) and out[5] == 2 * (64 * 256 + 64 * 128)  # two K + fp8 V stages
+    assert lib.fa_query_config(ctypes.byref(_params(shape=(1, 2, 128, 32), dtype=2)), out) == -3
+
+
 def test_validate_rejects_slices_over_2gib(lib):
     p = _params(shape=(1, 1, 9_000_000, 128))  # 9e6 rows x 256 B > 2 GiB
     assert lib.fa_validate(ctypes.byref(p)) == -2
@@ -145,6 +164,10 @@ def test_kernel_table_is_consistent(lib):
         for dt in ("float16", "bfloat16"):
             for c in (False, True):
                 assert (d, dt, c) in seen
+    for d in fa.FP8_V_HEAD_DIMS:
+        for dt in ("float16+float8_e5m2_v", "bfloat16+float8_e5m2_v"):
+            for c in (False, True):
+                assert (d, dt, c) in seen
 
 
 # ---------------------------------------------------------------------------
@@ -179,6 +202,18 @@ def test_validate_inputs_like_reference(shapes, msg):
     q, k, v = (torch.zeros(s, dtype=torch.float16) for s in shapes)
     with pytest.raises(ValueError, match=msg):
         fa._validate_inputs(q, k, v)
+
+
+def test_fp8_v_validation():
+    q = torch.zeros((1, 2, 8, 64), dtype=torch.bfloat16)
+    v8 = torch.zeros((1, 2, 8, 64), dtype=torch.float8_e5m2)
+    with pytest.raises(ValueError, match="GPU tensors"):  # accepted dtype mix, then the device check
+        fa._validate_inputs(q, q, v8)
+    q32 = torch.zeros((1, 2, 8, 32), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="float8_e5m2"):
+        fa._validate_inputs(q32, q32, torch.zeros((1, 2, 8, 32), dtype=torch.float8_e5m2))
+    with pytest.raises(ValueError, match="float16"):  # fp8 q / k are not accepted
+        fa._validate_inputs(v8, v8, v8)
 
 
 def test_rejects_cpu_tensors_and_bad_dtype():

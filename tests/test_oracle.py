@@ -322,3 +322,112 @@ def _merge_mutant_base2(parts):        # weights in base 2
 def test_partition_identity_rejects_merge_mutants(mutant):
     results = [_partition_check(mutant, causal=True, cuts=(0, 5, 16, 30, 37), scale=sc) for sc in (0.3, 40.0)]
     assert any(d_o > 1e-3 or d_l > 1e-3 for d_o, d_l in results)
+
+
+# ---------------------------------------------------------------------------
+# fp8-e5m2 V (reference flash_attention_forward.py:704, :737, :996)
+
+from oracle.attention_oracle import attention_fp8v, round_e5m2  # noqa: E402
+
+# (x, e5m2(x)) from the format: binade [2^e, 2^(e+1)) spaced 2^(e-2) for
+# e >= -14, subnormals spaced 2^-16, ties to the even mantissa, overflow to inf.
+E5M2_KAT = [
+    (1.0, 1.0), (1.125, 1.0), (1.1875, 1.25), (1.375, 1.5), (1.625, 1.5), (1.875, 2.0),
+    (-1.375, -1.5), (3.0, 3.0), (0.1, 0.09375), (57344.0, 57344.0), (60000.0, 57344.0),
+    (61439.0, 57344.0), (61440.0, math.inf), (1e9, math.inf), (-61440.0, -math.inf),
+    (2.0 ** -14, 2.0 ** -14), (1.5 * 2.0 ** -16, 2.0 ** -15), (2.0 ** -17, 0.0),
+    (0.75 * 2.0 ** -16, 2.0 ** -16), (1.25 * 2.0 ** -16, 2.0 ** -16), (0.0, 0.0),
+]
+
+
+def _e5m2_kat_holds(fn):
+    x = np.array([a for a, _ in E5M2_KAT], dtype=np.float32)
+    want = np.array([b for _, b in E5M2_KAT], dtype=np.float32)
+    return bool(np.array_equal(fn(x), want))
+
+
+def test_round_e5m2_known_values():
+    assert _e5m2_kat_holds(round_e5m2)
+
+
+def _e5m2_truncating(x):
+    x = np.asarray(x, dtype=np.float32)
+    ax = np.abs(x).astype(np.float64)
+    _, ex = np.frexp(np.where(ax > 0, ax, 1.0))
+    q = np.exp2(np.maximum(ex - 1.0, -14.0) - 2.0)
+    return np.copysign(np.floor(ax / q) * q, x).astype(np.float32)
+
+
+def _e5m2_no_subnormals(x):
+    r = round_e5m2(x)
+    return np.where(np.abs(r) < 2.0 ** -14, np.float32(0), r)
+
+
+@pytest.mark.parametrize("mutant", [_e5m2_truncating, _e5m2_no_subnormals])
+def test_e5m2_kat_rejects_mutants(mutant):
+    assert not _e5m2_kat_holds(mutant)
+
+
+def test_round_e5m2_matches_torch():
+    torch = pytest.importorskip("torch")
+    rs = np.random.RandomState(3)
+    x = np.concatenate([rs.standard_normal(100_000).astype(np.float32) * s
+                        for s in (1e-6, 1e-4, 1e-2, 1.0, 1e2, 1e4)]
+                       + [np.array([a for a, _ in E5M2_KAT], dtype=np.float32)])
+    want = torch.from_numpy(x).to(torch.float8_e5m2).float().numpy()
+    assert np.array_equal(round_e5m2(x), want)
+
+
+def _qkv(rs, shape):
+    q = rs.standard_normal(shape).astype(np.float32)
+    k = rs.standard_normal(shape).astype(np.float32)
+    v = round_e5m2(rs.standard_normal(shape).astype(np.float32))
+    return q, k, v
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("block_n,thr", [(64, 8.0), (16, 0.0), (7, 3.0)])
+def test_fp8v_replay_without_cast_is_attention(causal, block_n, thr):
+    # Online softmax over any tiling and any lazy threshold equals softmax.
+    rs = np.random.RandomState(4)
+    q, k, v = _qkv(rs, (2, 70, 64))
+    o, l = attention_fp8v(q, k, v, causal, 0.125, block_n=block_n, lazy_threshold=thr, round_p=False)
+    o_ref, l_ref = attention_ref(q, k, v, causal, 0.125)
+    assert np.abs(o - o_ref).max() < 2e-6 and np.abs(l - l_ref).max() < 2e-6
+
+
+def _probs(q, k, causal, scale):
+    s = (q.astype(np.float64) @ k.astype(np.float64).swapaxes(-1, -2)) * scale
+    if causal:
+        s = np.where(np.triu(np.ones(s.shape[-2:], dtype=bool), k=1), -np.inf, s)
+    s = s - s.max(axis=-1, keepdims=True)
+    e = np.exp(s)
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_fp8v_within_e5m2_bound_of_attention(causal):
+    # Rounding each p to nearest e5m2 moves it by at most 2^-3 p, so
+    # |O - O_ref| <= 2^-3 sum_j (p_j / l) |v_j| elementwise; l (and LSE) use
+    # the unrounded p.
+    rs = np.random.RandomState(5)
+    q, k, v = _qkv(rs, (2, 150, 64))
+    o, l = attention_fp8v(q, k, v, causal, 0.3)
+    o_ref, l_ref = attention_ref(q, k, v, causal, 0.3)
+    bound = 2.0 ** -3 * (_probs(q, k, causal, 0.3) @ np.abs(v).astype(np.float64)) + 1e-6
+    assert np.all(np.abs(o - o_ref) <= bound)
+    assert np.abs(o - o_ref).max() > 1e-4  # the cast is really applied
+    assert np.abs(l - l_ref).max() < 1e-5  # a few fp32 ulps at |LSE| ~ 8
+
+
+def test_fp8v_single_tile_closed_form():
+    # One tile with the exact row max: O = sum_j e5m2(2^(s_j c - m)) v_j / sum_j 2^(s_j c - m).
+    rs = np.random.RandomState(6)
+    q, k, v = _qkv(rs, (1, 40, 32))
+    o, _ = attention_fp8v(q, k, v, False, 0.25, block_n=40, lazy_threshold=0.0)
+    c = np.float32(np.float32(0.25) * np.float32(1.4426950408889634))
+    s = (q[0].astype(np.float64) @ k[0].astype(np.float64).T).astype(np.float32)
+    m = (s.max(axis=1) * c).astype(np.float32)
+    p = np.exp2((s.astype(np.float64) * np.float64(c) - m[:, None]).astype(np.float32)).astype(np.float32)
+    want = (round_e5m2(p).astype(np.float64) @ v[0]) / p.sum(axis=1, dtype=np.float32)[:, None]
+    assert np.abs(o[0] - want).max() < 1e-5
