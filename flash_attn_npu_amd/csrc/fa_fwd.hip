@@ -1033,7 +1033,13 @@ fa_fwd_dma_kernel(KernelArgs p) {
       l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
 
       // O^T += V^T P^T; the A operand is two transpose reads (keys +0..3 and
-      // +8..11 of the k-step), VPF fragments ahead of their MFMA.
+      // +8..11 of the k-step), VPF fragments ahead of their MFMA.  For
+      // D >= 128 the wave raises its issue priority over these MFMAs, so the
+      // other wave of the SIMD does not hold them back with its softmax
+      // (measured 1.5-2% on B4 H32 S2048 and B2 H16 S8192 causal; at D = 64
+      // it cost 2-4%, and raising it over the QK MFMAs or the softmax did not
+      // pay).
+      if constexpr (D >= 128) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < NPV; ++i) {
         if (i + VPF < NPV) vfr[i + VPF] = vread(i + VPF);
@@ -1046,6 +1052,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
       }
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, VPF, 0);
+      if constexpr (D >= 128) __builtin_amdgcn_s_setprio(0);
       }
     };
 
