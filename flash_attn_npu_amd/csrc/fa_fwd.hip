@@ -562,12 +562,16 @@ __device__ __forceinline__ int swz(int r) {
 // Chunk swizzle of fp8-e5m2 V rows (D bytes), read with ds_read_b64_tr_b8.
 // One read's half-wave touches rows {0..3, 8..11} of a 16-key step (+4 in
 // the upper half-wave), 8 bytes in each of two adjacent chunks per row:
-//  * D = 128 (two rows per 256-byte bank row): the four rows of one parity
-//    get distinct even chunk offsets, 2 ((r >> 1) & 1) + 4 ((r >> 3) & 1);
+//  * D = 256 (a row is one 256-byte bank row): the eight rows get distinct
+//    even chunk offsets, 2 ((r & 3) + 4 ((r >> 3) & 1));
+//  * D = 128 (two rows per bank row): the four rows of one parity get
+//    distinct even chunk offsets, 2 ((r >> 1) & 1) + 4 ((r >> 3) & 1);
 //  * D = 64 (four rows per bank row): rows r and r + 8 differ by 2 chunks.
 template <int D>
 __device__ __forceinline__ int swz8(int r) {
-  if constexpr (D == 128) {
+  if constexpr (D == 256) {
+    return ((r & 3) | (((r >> 3) & 1) << 2)) << 1;
+  } else if constexpr (D == 128) {
     return (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
   } else {
     static_assert(D == 64, "fp8 V head dim");
@@ -653,7 +657,7 @@ struct Cfg2 {
   static_assert(D == 16 || D == 32 || D == 64 || D == 128 || D == 256, "head dim");
   static_assert(IPT % NW == 0 && IPW >= 1, "DMA instructions must split evenly over waves");
   static_assert(VIPT % NW == 0 && VIPW >= 1, "DMA instructions must split evenly over waves");
-  static_assert(!V8 || ((D == 64 || D == 128) && BN == 64), "fp8 V: head dim 64 or 128, 64-key tiles");
+  static_assert(!V8 || ((D == 64 || D == 128 || D == 256) && BN == 64), "fp8 V: head dim 64, 128 or 256, 64-key tiles");
   static_assert(BN % 32 == 0, "tile shape");
   static_assert(NSTAGE == 2, "double-buffered: one tile computes while the next lands");
   static_assert(OCC == 1 || OCC == 2, "workgroups per CU");
@@ -822,6 +826,13 @@ fa_fwd_dma_kernel(KernelArgs p) {
       const uint32_t qo = (uint32_t)(qrow * p.q_ss * 2 + 16 * h);
 #pragma unroll
       for (int s = 0; s < D / 16; ++s) qf[s] = buf_load16(rq, qo + 32 * s) ^ p.q_sign;
+      // One workgroup per CU (D = 256, 16-bit V): Q lives in AGPRs (the MFMA
+      // reads its B operand from there), which leaves the VGPRs to S, P and the
+      // fragments.  (With fp8 V the 64-key S block takes those AGPRs.)
+      if constexpr (OCC == 1 && !V8) {
+#pragma unroll
+        for (int s = 0; s < D / 16; ++s) asm volatile("" : "+a"(qf[s]));
+      }
     }
 
     f32x16_t oacc[C::DB];
@@ -865,8 +876,14 @@ fa_fwd_dma_kernel(KernelArgs p) {
       tm_dma += td - tc;
 #endif
 
+      // A wave whose rows all precede this causal tile only issues its DMAs
+      // when another workgroup's wave shares its SIMD (OCC = 2).  With one
+      // workgroup per CU it computes the tile fully masked (p = 0) instead:
+      // the workgroup waits for its last wave either way, and the early exit
+      // cost the D = 256 kernels ~100 registers and scratch spills (masked
+      // tiles were ~10x slower).
       const int kbase = t * BN;
-      if (MASKED && CAUSAL && kbase > wave_last_q) {
+      if (MASKED && CAUSAL && OCC == 2 && kbase > wave_last_q) {
 #pragma unroll
         for (int i = 0; i < NDMA; ++i) dma(NEXT{}, rk_n, rv_n, i);
 #ifdef FA_TIMING
@@ -1676,6 +1693,7 @@ const KernelEntry kKernels[] = {
     FA_DMA_ENTRIES(16, 128, 4, 2, 2),
     FA_DMA8_ENTRIES(128, 64, 4, 2, 2),
     FA_DMA8_ENTRIES(64, 64, 4, 2, 2),
+    FA_DMA8_ENTRIES(256, 64, 4, 2, 1),
     FA_ENTRIES_DT_C(64, 64, 4),
     FA_ENTRIES_DT_C(128, 64, 4),
 };
@@ -1689,13 +1707,13 @@ bool is_valid_dtype(int dt) {
 bool v_is_fp8(int dt) { return dt == FA_DTYPE_FP16_V_E5M2 || dt == FA_DTYPE_BF16_V_E5M2; }
 bool out_is_bf16(int dt) { return dt == FA_DTYPE_BF16 || dt == FA_DTYPE_BF16_V_E5M2; }
 // Head dims of the fp8-V kernels.
-bool is_supported_fp8v_head_dim(int d) { return d == 64 || d == 128; }
+bool is_supported_fp8v_head_dim(int d) { return d == 64 || d == 128 || d == 256; }
 
 // Default (BLOCK_N, waves) per head dim; BLOCK_M = 32 * waves.
 void default_tiling(int D, int dtype, int causal, int *bn, int *nw) {
-  (void)dtype;
   (void)causal;
-  *bn = D == 16 ? 128 : (D == 256 ? 32 : 64);
+  // fp8 V: 64-key tiles, one 32x32x64 MFMA per 32 head dims.
+  *bn = v_is_fp8(dtype) ? 64 : (D == 16 ? 128 : (D == 256 ? 32 : 64));
   *nw = 4;
 }
 

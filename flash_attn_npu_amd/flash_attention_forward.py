@@ -71,7 +71,7 @@ FA_DTYPE = {torch.float16: 0, torch.bfloat16: 1}
 # (FA_DTYPE_FP16_V_E5M2 = 2, FA_DTYPE_BF16_V_E5M2 = 3).
 FP8_V_DTYPE = torch.float8_e5m2
 FA_DTYPE_V_E5M2_OFFSET = 2
-FP8_V_HEAD_DIMS = (64, 128)
+FP8_V_HEAD_DIMS = (64, 128, 256)
 FP8_V_TILING = (128, 64)
 _DTYPE_NAMES = {0: "float16", 1: "bfloat16", 2: "float16+float8_e5m2_v", 3: "bfloat16+float8_e5m2_v"}
 

@@ -109,9 +109,9 @@ def test_validate_rejects(lib, mutate, code):
 def test_validate_fp8_v(lib):
     # dtype 2 / 3: fp16 / bf16 q, k, o with an fp8-e5m2 v (head dims 64 and 128).
     for dt in (2, 3):
-        for d in (64, 128):
+        for d in (64, 128, 256):
             assert lib.fa_validate(ctypes.byref(_params(shape=(1, 2, 128, d), dtype=dt))) == 0, (dt, d)
-        for d in (16, 32, 256):
+        for d in (16, 32):
             assert lib.fa_validate(ctypes.byref(_params(shape=(1, 2, 128, d), dtype=dt))) == -3, (dt, d)
     # 16-byte rows: an fp8 v needs strides in multiples of 16 elements.
     p = _params(shape=(1, 2, 128, 64), dtype=3)
@@ -123,6 +123,11 @@ def test_validate_fp8_v(lib):
     assert lib.fa_query_config(ctypes.byref(_params(shape=(4, 32, 2048, 128), dtype=3)), out) == 0
     assert (out[0], out[1]) == (128, 64) and out[5] == 2 * (64 * 256 + 64 * 128)  # two K + fp8 V stages
     assert lib.fa_query_config(ctypes.byref(_params(shape=(1, 2, 128, 32), dtype=2)), out) == -3
+    # D = 256: 64-key tiles with fp8 V (32 with a 16-bit V), one workgroup per CU.
+    assert lib.fa_query_config(ctypes.byref(_params(shape=(1, 2, 4096, 256), dtype=3)), out) == 0
+    assert out[1] == 64 and out[5] == 2 * (64 * 512 + 64 * 256)
+    assert lib.fa_query_config(ctypes.byref(_params(shape=(1, 2, 4096, 256), dtype=1)), out) == 0
+    assert out[1] == 32
 
 
 def test_validate_rejects_slices_over_2gib(lib):

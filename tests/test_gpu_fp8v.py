@@ -90,7 +90,7 @@ def _run(fa, q, k, v, causal, scale, **kw):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
 @pytest.mark.parametrize("s", [1, 64, 130, 257])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 128, 256])
 def test_fp8v_matches_replay(fa, d, causal, s, dtype):
     print(f"[fp8v] D={d} causal={causal} S={s} {dtype}", flush=True)
     q, k, v = _inputs(100 + d + s + causal, (1, 2, s, d), dtype)

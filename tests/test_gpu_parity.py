@@ -171,6 +171,8 @@ def test_every_kernel_instance(fa):
     """Each BM/BN variant in the library, forced through the BM/BN override."""
     g = torch.Generator().manual_seed(10)
     for row in fa.kernel_table():
+        if "float8" in row["dtype"]:
+            continue  # the fp8-V kernels: every one runs in tests/test_gpu_fp8v.py (its D x mask x dtype grid)
         dtype = torch.float16 if row["dtype"] == "float16" else torch.bfloat16
         d, causal = row["HEAD_DIM"], row["causal"]
         _say(f"[kernel] {row}")
