@@ -55,7 +55,7 @@ DEFAULT_TILING_PRESETS = {
     (128, 8, 2048, 128, True): (128, 32),
     (128, 8, 2048, 256, False): (128, 32),
     (128, 8, 4096, 128, False): (128, 32),
-    (128, 8, 8192, 64, False): (128, 64),
+    (128, 8, 8192, 64, False): (128, 128),
 }
 # END AUTO-TUNED DEFAULT TILING PRESETS
 
