@@ -567,15 +567,20 @@ __device__ __forceinline__ int swz(int r) {
 //  * D = 128 (two rows per bank row): the four rows of one parity get
 //    distinct even chunk offsets, 2 ((r >> 1) & 1) + 4 ((r >> 3) & 1);
 //  * D = 64 (four rows per bank row): rows r and r + 8 differ by 2 chunks.
+//  * D = 32 (eight rows per bank row): rows r and r + 8 share their banks
+//    whatever the chunk order, so the read takes two passes; no swizzle;
+//  * D = 16: one chunk per row, no swizzle (rows 0..15 fill a bank row).
 template <int D>
 __device__ __forceinline__ int swz8(int r) {
   if constexpr (D == 256) {
     return ((r & 3) | (((r >> 3) & 1) << 2)) << 1;
   } else if constexpr (D == 128) {
     return (((r >> 1) & 1) << 1) | (((r >> 3) & 1) << 2);
-  } else {
-    static_assert(D == 64, "fp8 V head dim");
+  } else if constexpr (D == 64) {
     return ((r >> 3) & 1) << 1;
+  } else {
+    static_assert(D == 32 || D == 16, "fp8 V head dim");
+    return 0;
   }
 }
 
@@ -647,17 +652,21 @@ struct Cfg2 {
   static constexpr int VRPI = 1024 / VROW;
   static constexpr int VTILE = BN * VROW;
   static constexpr int VIPT = VTILE / 1024;
-  static constexpr int VIPW = VIPT / NW;
+  // An fp8 V tile of D <= 32 is less than one DMA instruction per wave: every
+  // wave still issues one, the extra waves fetch the rows after the tile
+  // (in range, or zeros past Sk) into LDS padding that is never read.
+  static constexpr int VIPW = VIPT >= NW ? VIPT / NW : 1;
+  static constexpr int VTILE_LDS = VIPW * NW * 1024;
   static constexpr int NDMA = IPW + VIPW;     // DMA instructions per wave and tile
-  static constexpr int STAGE = TILE + VTILE;
+  static constexpr int STAGE = TILE + VTILE_LDS;
   static constexpr int LDS_BYTES = NSTAGE * STAGE;
   // O^T blocks of 32 head dims; D = 16 uses one block whose upper 16 rows
   // come out zero (the V^T operand rows past D are zeroed).
   static constexpr int DB = D >= 32 ? D / 32 : 1;
   static_assert(D == 16 || D == 32 || D == 64 || D == 128 || D == 256, "head dim");
   static_assert(IPT % NW == 0 && IPW >= 1, "DMA instructions must split evenly over waves");
-  static_assert(VIPT % NW == 0 && VIPW >= 1, "DMA instructions must split evenly over waves");
-  static_assert(!V8 || ((D == 64 || D == 128 || D == 256) && BN == 64), "fp8 V: head dim 64, 128 or 256, 64-key tiles");
+  static_assert(VIPT % NW == 0 || (V8 && VIPT < NW), "DMA instructions must split evenly over waves");
+  static_assert(!V8 || (BN % 64 == 0 && (D >= 32 ? BN == 64 : BN == 128)), "fp8 V: 64-key tiles (D = 16: 128)");
   static_assert(BN % 32 == 0, "tile shape");
   static_assert(NSTAGE == 2, "double-buffered: one tile computes while the next lands");
   static_assert(OCC == 1 || OCC == 2, "workgroups per CU");
@@ -730,7 +739,9 @@ fa_fwd_dma_kernel(KernelArgs p) {
     const int row = 8 * (q >> 2) + 4 * (g >> 1) + (q & 3);
 #pragma unroll
     for (int db = 0; db < C::DB; ++db) {
-      const int lc = 2 * db + (g & 1);
+      // D = 16: lanes of the upper 16 dims re-read dims 0..15 (in the row)
+      // and their fragments are zeroed before use.
+      const int lc = 2 * db + (D >= 32 ? (g & 1) : 0);
       vro[db][0] = (uint32_t)(row * C::VROW + ((lc ^ swz8<D>(row)) * 16) + (sl & 1) * 8);
     }
   } else {
@@ -907,17 +918,21 @@ fa_fwd_dma_kernel(KernelArgs p) {
       // reads so they land during the softmax.
       constexpr int NQK = (D / 16) * (BN / 32);
       constexpr int KPF = 4;
-      constexpr int NPV = V8 ? C::DB : (BN / 16) * C::DB;
+      constexpr int NPV = V8 ? (BN / 64) * C::DB : (BN / 16) * C::DB;
       constexpr int VPF = V8 ? 1 : 2;
       constexpr int VRD = V8 ? 4 : 2;  // LDS reads per V^T fragment
-      // fp8 V^T fragment of head dims 32db.. for all 64 keys (32 bytes per lane).
-      auto vread8 = [&](int db) {
+      // fp8 V^T fragment i = (64-key chunk kc, head dims 32db..): 32 bytes per lane.
+      auto vread8 = [&](int i) {
+        const int kc = i / C::DB, db = i % C::DB;
         i32x8_t f;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          const u32x2_t x = lds_read_tr8(sbase, vro[db][0] + (uint32_t)(C::TILE + 16 * u * C::VROW));
+          const u32x2_t x = lds_read_tr8(sbase, vro[db][0] + (uint32_t)(C::TILE + (64 * kc + 16 * u) * C::VROW));
           f[2 * u] = (int)x[0];
           f[2 * u + 1] = (int)x[1];
+        }
+        if constexpr (D < 32) {
+          if (lane & 16) f = (i32x8_t){0, 0, 0, 0, 0, 0, 0, 0};
         }
         return f;
       };
@@ -1015,22 +1030,26 @@ fa_fwd_dma_kernel(KernelArgs p) {
         }
 
       if constexpr (V8) {
-        // P^T in e5m2 (round to nearest even): byte j = register j % 16 of
-        // block j / 16, four bytes per VGPR.
-        i32x8_t pf8;
+        // P^T in e5m2 (round to nearest even), per 64-key chunk kc: byte j =
+        // register j % 16 of block 2kc + j / 16, four bytes per VGPR.
+        i32x8_t pf8[BN / 64];
 #pragma unroll
-        for (int w = 0; w < 8; ++w) {
-          const int kb = w >> 2, r0 = 4 * (w & 3);
-          const int lo = __builtin_amdgcn_cvt_pk_bf8_f32(sacc[kb][r0], sacc[kb][r0 + 1], 0, false);
-          pf8[w] = __builtin_amdgcn_cvt_pk_bf8_f32(sacc[kb][r0 + 2], sacc[kb][r0 + 3], lo, true);
-        }
+        for (int kc = 0; kc < BN / 64; ++kc)
+#pragma unroll
+          for (int w = 0; w < 8; ++w) {
+            const int kb = 2 * kc + (w >> 2), r0 = 4 * (w & 3);
+            const int lo = __builtin_amdgcn_cvt_pk_bf8_f32(sacc[kb][r0], sacc[kb][r0 + 1], 0, false);
+            pf8[kc][w] = __builtin_amdgcn_cvt_pk_bf8_f32(sacc[kb][r0 + 2], sacc[kb][r0 + 3], lo, true);
+          }
         l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
-        // O^T += V^T P^T: one fp8 MFMA per 32 head dims (unit scales: E8M0
-        // exponent 127 = 2^0), the next fragment's four reads ahead of it.
+        // O^T += V^T P^T: one fp8 MFMA per (64 keys, 32 head dims) (unit
+        // scales: E8M0 exponent 127 = 2^0), the next fragment's four reads
+        // ahead of it.
 #pragma unroll
-        for (int db = 0; db < NPV; ++db) {
-          if (db + VPF < NPV) vfr8[db + VPF] = vread8(db + VPF);
-          oacc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vfr8[db], pf8, oacc[db], 1, 1, 0, 127, 0, 127);
+        for (int i = 0; i < NPV; ++i) {
+          if (i + VPF < NPV) vfr8[i + VPF] = vread8(i + VPF);
+          const int kc = i / C::DB, db = i % C::DB;
+          oacc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vfr8[i], pf8[kc], oacc[db], 1, 1, 0, 127, 0, 127);
         }
 #pragma unroll
         for (int i = 0; i < NPV - VPF; ++i) {
@@ -1698,6 +1717,8 @@ const KernelEntry kKernels[] = {
     FA_DMA8_ENTRIES(128, 64, 4, 2, 2),
     FA_DMA8_ENTRIES(64, 64, 4, 2, 2),
     FA_DMA8_ENTRIES(256, 64, 4, 2, 1),
+    FA_DMA8_ENTRIES(32, 64, 4, 2, 2),
+    FA_DMA8_ENTRIES(16, 128, 4, 2, 2),
     FA_ENTRIES_DT_C(64, 64, 4),
     FA_ENTRIES_DT_C(128, 64, 4),
 };
@@ -1711,13 +1732,14 @@ bool is_valid_dtype(int dt) {
 bool v_is_fp8(int dt) { return dt == FA_DTYPE_FP16_V_E5M2 || dt == FA_DTYPE_BF16_V_E5M2; }
 bool out_is_bf16(int dt) { return dt == FA_DTYPE_BF16 || dt == FA_DTYPE_BF16_V_E5M2; }
 // Head dims of the fp8-V kernels.
-bool is_supported_fp8v_head_dim(int d) { return d == 64 || d == 128 || d == 256; }
+bool is_supported_fp8v_head_dim(int d) { return is_supported_head_dim(d); }
 
 // Default (BLOCK_N, waves) per head dim; BLOCK_M = 32 * waves.
 void default_tiling(int D, int dtype, int causal, int *bn, int *nw) {
   (void)causal;
-  // fp8 V: 64-key tiles, one 32x32x64 MFMA per 32 head dims.
-  *bn = v_is_fp8(dtype) ? 64 : ((D == 16 || D == 64) ? 128 : (D == 256 ? 32 : 64));
+  // fp8 V: 64-key tiles (D = 16: 128), one 32x32x64 MFMA per 64 keys and 32
+  // head dims.
+  *bn = v_is_fp8(dtype) ? (D == 16 ? 128 : 64) : ((D == 16 || D == 64) ? 128 : (D == 256 ? 32 : 64));
   *nw = 4;
 }
 

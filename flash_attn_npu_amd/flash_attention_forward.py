@@ -71,8 +71,13 @@ FA_DTYPE = {torch.float16: 0, torch.bfloat16: 1}
 # (FA_DTYPE_FP16_V_E5M2 = 2, FA_DTYPE_BF16_V_E5M2 = 3).
 FP8_V_DTYPE = torch.float8_e5m2
 FA_DTYPE_V_E5M2_OFFSET = 2
-FP8_V_HEAD_DIMS = (64, 128, 256)
-FP8_V_TILING = (128, 64)
+FP8_V_HEAD_DIMS = (16, 32, 64, 128, 256)
+
+
+def fp8_v_tiling(head_dim):
+    """(BLOCK_M, BLOCK_N) of the fp8-V kernels: 64-key tiles, 128 at D = 16."""
+    return (128, 128) if head_dim == 16 else (128, 64)
+
 _DTYPE_NAMES = {0: "float16", 1: "bfloat16", 2: "float16+float8_e5m2_v", 3: "bfloat16+float8_e5m2_v"}
 
 
@@ -322,7 +327,7 @@ def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
     fp8_v = v.dtype == FP8_V_DTYPE
     bm, bn, source = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn)
     if fp8_v and source != "override":
-        bm, bn = FP8_V_TILING  # the fp8-V kernels' one tiling; presets are for 16-bit V
+        bm, bn = fp8_v_tiling(head_dim)  # the fp8-V kernels' one tiling; presets are for 16-bit V
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     out = torch.empty_like(q)
     lse = torch.empty((z, h, n_ctx), device=q.device, dtype=torch.float32)

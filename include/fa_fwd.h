@@ -19,7 +19,7 @@
  *    row, and the base pointers 16-byte aligned (128-bit loads and stores).
  *    One (batch, head) slice of a tensor must span less than 2 GiB.
  *  - q, k and o share one element type, fp16 or bf16; v has that type too,
- *    or is fp8-e5m2 (FA_DTYPE_*_V_E5M2, head dims 64, 128, 256; v strides then
+ *    or is fp8-e5m2 (FA_DTYPE_*_V_E5M2, every head dim; v strides then
  *    multiples of 16 elements).  lse is fp32,
  *    contiguous [B, H, Sq], natural log, over the scaled logits
  *    (lse[i] = log(sum_j exp(sm_scale * q_i . k_j)) over the visible keys),

@@ -107,12 +107,11 @@ def test_validate_rejects(lib, mutate, code):
 
 
 def test_validate_fp8_v(lib):
-    # dtype 2 / 3: fp16 / bf16 q, k, o with an fp8-e5m2 v (head dims 64 and 128).
+    # dtype 2 / 3: fp16 / bf16 q, k, o with an fp8-e5m2 v, every head dim.
     for dt in (2, 3):
-        for d in (64, 128, 256):
+        for d in (16, 32, 64, 128, 256):
             assert lib.fa_validate(ctypes.byref(_params(shape=(1, 2, 128, d), dtype=dt))) == 0, (dt, d)
-        for d in (16, 32):
-            assert lib.fa_validate(ctypes.byref(_params(shape=(1, 2, 128, d), dtype=dt))) == -3, (dt, d)
+        assert lib.fa_validate(ctypes.byref(_params(shape=(1, 2, 128, 48), dtype=dt))) == -3
     # 16-byte rows: an fp8 v needs strides in multiples of 16 elements.
     p = _params(shape=(1, 2, 128, 64), dtype=3)
     p.v_stride[2] = 72
@@ -122,7 +121,10 @@ def test_validate_fp8_v(lib):
     out = (ctypes.c_int32 * 8)()
     assert lib.fa_query_config(ctypes.byref(_params(shape=(4, 32, 2048, 128), dtype=3)), out) == 0
     assert (out[0], out[1]) == (128, 64) and out[5] == 2 * (64 * 256 + 64 * 128)  # two K + fp8 V stages
-    assert lib.fa_query_config(ctypes.byref(_params(shape=(1, 2, 128, 32), dtype=2)), out) == -3
+    assert lib.fa_query_config(ctypes.byref(_params(shape=(1, 2, 128, 32), dtype=2)), out) == 0
+    assert out[1] == 64 and out[5] == 2 * (64 * 64 + 4 * 1024)  # 2 KB fp8 V tile padded to a DMA per wave
+    assert lib.fa_query_config(ctypes.byref(_params(shape=(1, 2, 128, 16), dtype=2)), out) == 0
+    assert out[1] == 128 and out[5] == 2 * (128 * 32 + 4 * 1024)
     # D = 256: 64-key tiles with fp8 V (32 with a 16-bit V), one workgroup per CU.
     assert lib.fa_query_config(ctypes.byref(_params(shape=(1, 2, 4096, 256), dtype=3)), out) == 0
     assert out[1] == 64 and out[5] == 2 * (64 * 512 + 64 * 256)
@@ -214,9 +216,9 @@ def test_fp8_v_validation():
     v8 = torch.zeros((1, 2, 8, 64), dtype=torch.float8_e5m2)
     with pytest.raises(ValueError, match="GPU tensors"):  # accepted dtype mix, then the device check
         fa._validate_inputs(q, q, v8)
-    q32 = torch.zeros((1, 2, 8, 32), dtype=torch.bfloat16)
-    with pytest.raises(ValueError, match="float8_e5m2"):
-        fa._validate_inputs(q32, q32, torch.zeros((1, 2, 8, 32), dtype=torch.float8_e5m2))
+    q48 = torch.zeros((1, 2, 8, 48), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="HEAD_DIM"):
+        fa._validate_inputs(q48, q48, torch.zeros((1, 2, 8, 48), dtype=torch.float8_e5m2))
     with pytest.raises(ValueError, match="float16"):  # fp8 q / k are not accepted
         fa._validate_inputs(v8, v8, v8)
 

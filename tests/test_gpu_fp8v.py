@@ -5,7 +5,8 @@ With V in float8_e5m2 the kernel, like the reference, rounds the unnormalised
 probabilities of each KV tile to e5m2 before P.V (and sums the unrounded ones
 into l).  Where that rounding lands depends on the tiling and on when the
 running max moves, so the oracle replays the kernel's schedule
-(`attention_fp8v`: 64-key tiles, max moved only past a 2^8 margin).  Gates:
+(`attention_fp8v`: 64-key tiles, 128 at D = 16, max moved only past a 2^8
+margin).  Gates:
 
 * LSE: max|dLSE| <= 1e-3 against both the replay and the fp32 formula (l uses
   unrounded p, so the fp8 cast does not touch it).
@@ -56,7 +57,8 @@ def _check_head(qh, kh, vh, og, lg, causal, scale, dtype, schedule_check=True):
     """Gates for one (b, h); returns (max|dO| vs replay, rows over tol, max|dLSE|)."""
     dt = DT_ORACLE[dtype]
     tol = O_TOL[dtype]
-    r8, rl8 = attention_fp8v(qh, kh, vh, causal, scale, out_dtype=dt)
+    bn = 128 if qh.shape[-1] == 16 else 64  # the fp8-V kernels' key tile
+    r8, rl8 = attention_fp8v(qh, kh, vh, causal, scale, out_dtype=dt, block_n=bn)
     ref, rl = attention_ref(qh, kh, vh, causal, scale, out_dtype=dt)
     p = _probs(qh, kh, causal, scale)
     av = np.abs(vh).astype(np.float64)
@@ -70,7 +72,7 @@ def _check_head(qh, kh, vh, og, lg, causal, scale, dtype, schedule_check=True):
     dl = max(float(np.abs(lg - rl8).max()), float(np.abs(lg - rl).max()))
     assert dl <= LSE_TOL
     if schedule_check:
-        r0, _ = attention_fp8v(qh, kh, vh, causal, scale, out_dtype=dt, lazy_threshold=0.0)
+        r0, _ = attention_fp8v(qh, kh, vh, causal, scale, out_dtype=dt, block_n=bn, lazy_threshold=0.0)
         gap = np.abs(r0 - r8).mean()
         if gap > 1e-4:
             # Both distances share the output-rounding floor (~1e-3 for bf16
@@ -90,7 +92,7 @@ def _run(fa, q, k, v, causal, scale, **kw):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
 @pytest.mark.parametrize("s", [1, 64, 130, 257])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
-@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("d", [16, 32, 64, 128, 256])
 def test_fp8v_matches_replay(fa, d, causal, s, dtype):
     print(f"[fp8v] D={d} causal={causal} S={s} {dtype}", flush=True)
     q, k, v = _inputs(100 + d + s + causal, (1, 2, s, d), dtype)
