@@ -1396,8 +1396,12 @@ fa_fwd_pp_kernel(KernelArgs p) {
 #endif
     };
 
-    // M(t): PV(t-1) then QK(t), operand reads MPF MFMAs ahead.
+    // M(t): PV(t-1) then QK(t), operand reads MPF MFMAs ahead.  The wave
+    // raises its issue priority for the phase, so the other group's softmax
+    // fills the gaps between its MFMAs instead of delaying them (4-5% on
+    // B4 H32 S2048, B2 H16 S8192 and B8 H32 S3000 causal).
     auto mphase = [&](int t, auto pv_tag, auto qk_tag) {
+      __builtin_amdgcn_s_setprio(1);
       constexpr bool DO_PV = decltype(pv_tag)::value;
       constexpr bool DO_QK = decltype(qk_tag)::value;
       constexpr int NPV = DO_PV ? (BN / 16) * (D / 32) : 0;
@@ -1450,6 +1454,7 @@ fa_fwd_pp_kernel(KernelArgs p) {
         else __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
       }
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, MPF < NOPS ? MPF : NOPS, 0);
+      __builtin_amdgcn_s_setprio(0);
     };
 
     // S(t): mask (diagonal / ragged tail only), online softmax, rescale O, P(t).
