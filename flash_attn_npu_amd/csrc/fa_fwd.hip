@@ -8,9 +8,10 @@
 // :1022-1033) computes on Ascend.  The work decomposition is gfx950-native:
 //
 //  * A workgroup owns BM = 32*NW query rows of one (b, h); each of its NW
-//    wave64s owns 32 of them.  K and V tiles of BN keys are streamed through
-//    double-buffered LDS; the next tile's global loads (128-bit) are in flight
-//    while the current tile is computed, so one barrier per tile suffices.
+//    wave64s owns 32 of them.  K and V tiles of BN keys reach LDS by direct
+//    DMA (buffer_load ... lds) into a ring of NSTAGE stages, so tile
+//    t + NSTAGE - 1 is in flight while tile t is computed and one barrier
+//    per tile suffices.
 //  * Both products run on v_mfma_f32_32x32x16_{bf16,f16} with fp32
 //    accumulation, in transposed form:  S^T = K Q^T  and  O^T = V^T P^T.
 //    In the 32x32 accumulator layout lane l holds column l%32, so every lane
@@ -18,10 +19,13 @@
 //    in-lane reductions plus one v_permlane32_swap, the rescale factor is a
 //    per-lane scalar, and P^T leaves the S^T accumulator already in the
 //    B-operand layout of the second MFMA (no LDS round trip for P).
-//  * V is written to LDS transposed (V^T, key order permuted to match the
-//    accumulator layout, XOR-swizzled 16-byte chunks) so that the A operand of
-//    O^T = V^T P^T is one conflict-free ds_read_b128 per lane.
-//  * Q stays in VGPRs for the whole tile loop.  sm_scale*log2(e) is applied in
+//  * K and V stay row-major in LDS with XOR-swizzled 16-byte chunks; K is
+//    read with ds_read_b128 and V^T with the gfx950 transpose read
+//    ds_read_b64_tr_b16, so no VGPR or VALU is spent moving or transposing
+//    tiles.  With V in fp8-e5m2, P is rounded to e5m2 and O^T = V^T P^T runs
+//    on the scaled 32x32x64 fp8 MFMA (V^T read with ds_read_b64_tr_b8).
+//  * Q stays in registers for the whole tile loop (AGPRs at D = 256, where
+//    one wave per SIMD holds 512 registers).  sm_scale*log2(e) is applied in
 //    fp32 after the MFMA (exp2 path); Q is never pre-scaled or re-rounded.
 //  * The running max is always kept (numerically stable), with a lazy update:
 //    it only moves when a new row max exceeds it by more than 2^8, so the
@@ -30,10 +34,11 @@
 //    waves skip tiles above their own diagonal, and only tiles crossing the
 //    diagonal or the ragged key tail evaluate the mask.  Ragged query/key
 //    tails are zero-filled on load, masked to -inf, and never stored.
-//  * Grid: one workgroup per (b, h, m-tile); consecutive logical tiles are
-//    kept on one XCD (workgroups are dispatched round-robin over the 8 XCDs)
-//    so the m-tiles of a head share that XCD's L2, and causal tiles of a head
-//    run heaviest first.
+//  * Grid: persistent (as many workgroups as are resident at once); the
+//    workgroups of each XCD pull (head, m-tile) tiles, heaviest first, from
+//    a tile queue that owns a fixed set of heads, so a head's K/V is read
+//    through one L2.  Grids too small to fill the chip split the keys
+//    (split-KV) and merge the partial results in a second kernel.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -259,267 +264,8 @@ struct TileQueue {
   }
 };
 
-template <int D, int BN, int NW, bool BF16, bool CAUSAL>
-struct FaConfig {
-  static constexpr int BM = 32 * NW;           // query rows per workgroup
-  static constexpr int NT = 64 * NW;           // threads per workgroup
-  static constexpr int DCH = D / 8;            // 16-byte chunks per K/V row
-  static constexpr int NKG = NT / DCH;         // key groups loaded per pass
-  static constexpr int CPT = BN / NKG;         // keys per thread per tile
-  static constexpr int RK = D * 2 + 16;        // LDS bytes per K row (padded)
-  static constexpr int RV = BN * 2 + 16;       // LDS bytes per V^T row (padded)
-  static constexpr int NCH = BN / 8;           // 16-byte chunks per V^T row
-  static constexpr int K_BYTES = BN * RK;
-  static constexpr int V_BYTES = D * RV;
-  static constexpr int STAGE_BYTES = K_BYTES + V_BYTES;
-  static constexpr int LDS_BYTES = 2 * STAGE_BYTES;
-  static_assert(D % 32 == 0, "head dim must be a multiple of 32");
-  static_assert(BN % 32 == 0, "BN must be a multiple of 32");
-  static_assert(NT % DCH == 0, "threads must tile the chunk columns");
-  static_assert(NKG * CPT == BN && CPT >= 1 && CPT <= 4 && (4 % CPT) == 0,
-                "each thread loads 1, 2 or 4 keys of one 4-key group");
-  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of one gfx950 CU");
-};
-
-template <int D, int BN, int NW, bool BF16, bool CAUSAL>
-__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
-fa_fwd_kernel(KernelArgs p) {
-  using C = FaConfig<D, BN, NW, BF16, CAUSAL>;
-  constexpr int BM = C::BM;
-  __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n = lane & 31;   // query column of this lane (and MFMA A-operand row)
-  const int h = lane >> 5;   // lane half
-
-  // Loader mapping: thread -> (16-byte column chunk, group of CPT keys).
-  const int ld_dc = tid % C::DCH;
-  const int ld_kg = tid / C::DCH;
-  // Byte offsets of this thread's CPT rows inside a K/V tile (tile-invariant).
-  uint32_t koff[C::CPT], voff[C::CPT];
-#pragma unroll
-  for (int j = 0; j < C::CPT; ++j) {
-    koff[j] = (uint32_t)((ld_kg * C::CPT + j) * p.k_ss * 2 + 16 * ld_dc);
-    voff[j] = (uint32_t)((ld_kg * C::CPT + j) * p.v_ss * 2 + 16 * ld_dc);
-  }
-  // LDS byte offsets (within a stage) written by this thread.
-  const uint32_t k_wr = (uint32_t)((ld_kg * C::CPT) * C::RK + 16 * ld_dc);
-  const int pos0 = vt_pos(ld_kg * C::CPT);
-  const uint32_t v_wr = (uint32_t)(C::K_BYTES + (8 * ld_dc) * C::RV +
-                                   (((pos0 >> 3) ^ (ld_dc & (C::NCH - 1))) * 16) + (pos0 & 7) * 2);
-  // LDS byte offsets read by this lane for the A operands.
-  const uint32_t k_rd = (uint32_t)(n * C::RK + h * 16);
-
-  const float c = p.c;
-
-  // Tile loop: thread 0 takes tickets (the next one is requested at the top
-  // of a tile and published through LDS at its end, behind a barrier).
-  __shared__ uint32_t s_ticket[2];
-  const TileQueue tq(p);
-  int bh, mt, split;
-  for (int it = 0; tq.tile(it == 0 ? tq.first() : s_ticket[it & 1], p.n_mtiles, CAUSAL, p.q_group, p.q_bands,
-                           &bh, &mt, &split);
-       ++it) {
-    unsigned long long next_raw = 0;
-    if (threadIdx.x == 0) next_raw = tq.request();
-    const int bb = bh / p.H;
-    const int hh = bh - bb * p.H;
-
-    const int q0 = mt * BM;
-    const int q0w = q0 + 32 * wave;
-    const int qrow = q0w + n;
-
-    const char *qg = p.q + 2 * (bb * p.q_sb + hh * p.q_sh);
-    const char *kg = p.k + 2 * (bb * p.k_sb + hh * p.k_sh);
-    const char *vg = p.v + 2 * (bb * p.v_sb + hh * p.v_sh);
-
-    // Q^T fragments (B operand of S^T = K Q^T): lane (h, n) holds
-    // Q[qrow][16s + 8h .. +8] for every 16-wide d-step s.  Rows >= Sq read 0.
-    u32x4_t qf[D / 16];
-    {
-      const BufRsrc rq = make_rsrc(qg, (uint32_t)((int64_t)p.Sq * p.q_ss * 2));
-      const uint32_t qo = (uint32_t)(qrow * p.q_ss * 2 + 16 * h);
-#pragma unroll
-      for (int s = 0; s < D / 16; ++s) qf[s] = buf_load16(rq, qo + 32 * s) ^ p.q_sign;
-    }
-
-    const int kv_end = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
-    const int n_tiles = (kv_end + BN - 1) / BN;
-    const int wave_last_q = q0w + 31;
-
-    u32x4_t kreg[C::CPT], vreg[C::CPT];
-    // Global -> registers for tile t; keys >= Sk fall outside the buffer
-    // range and read as zero.
-    auto gload = [&](int t) {
-      const int key0 = t * BN;
-      const BufRsrc rk = make_rsrc(kg + (int64_t)key0 * p.k_ss * 2,
-                                   (uint32_t)((int64_t)(p.Sk - key0) * p.k_ss * 2));
-      const BufRsrc rv = make_rsrc(vg + (int64_t)key0 * p.v_ss * 2,
-                                   (uint32_t)((int64_t)(p.Sk - key0) * p.v_ss * 2));
-#pragma unroll
-      for (int j = 0; j < C::CPT; ++j) {
-        kreg[j] = buf_load16(rk, koff[j]);
-        vreg[j] = buf_load16(rv, voff[j]);
-      }
-    };
-    // Registers -> LDS stage `buf`: K row-major, V transposed to V^T.
-    auto swrite = [&](int buf) {
-      char *st = smem + buf * C::STAGE_BYTES;
-#pragma unroll
-      for (int j = 0; j < C::CPT; ++j) *(u32x4_t *)(st + k_wr + j * C::RK) = kreg[j];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        char *dst = st + v_wr + i * C::RV;
-        const int w = i >> 1, sh = (i & 1) * 16;
-        if constexpr (C::CPT == 4) {
-          u32x2_t x;
-          x[0] = ((vreg[0][w] >> sh) & 0xffffu) | (((vreg[1][w] >> sh) & 0xffffu) << 16);
-          x[1] = ((vreg[2][w] >> sh) & 0xffffu) | (((vreg[3][w] >> sh) & 0xffffu) << 16);
-          *(u32x2_t *)dst = x;
-        } else if constexpr (C::CPT == 2) {
-          *(uint32_t *)dst = ((vreg[0][w] >> sh) & 0xffffu) | (((vreg[1][w] >> sh) & 0xffffu) << 16);
-        } else {
-          *(uint16_t *)dst = (uint16_t)((vreg[0][w] >> sh) & 0xffffu);
-        }
-      }
-    };
-
-    f32x16_t oacc[D / 32];
-#pragma unroll
-    for (int db = 0; db < D / 32; ++db) oacc[db] = (f32x16_t){};
-    float m_run = -INFINITY;  // running max, in scaled log2 units
-    float l_run = 0.f;        // this lane-half's partial row sum
-
-    if (n_tiles > 0) gload(0);
-    for (int t = 0; t < n_tiles; ++t) {
-      const int buf = t & 1;
-      swrite(buf);
-      __syncthreads();
-      if (t + 1 < n_tiles) gload(t + 1);
-
-      const int kbase = t * BN;
-      if (CAUSAL && kbase > wave_last_q) continue;  // whole tile above this wave's diagonal
-
-      const char *ks = smem + buf * C::STAGE_BYTES;
-      const char *vs = ks + C::K_BYTES;
-
-      // S^T = K Q^T: block kb covers keys kbase + 32kb .. +32.
-      f32x16_t sacc[BN / 32];
-#pragma unroll
-      for (int kb = 0; kb < BN / 32; ++kb) {
-        sacc[kb] = (f32x16_t){};
-#pragma unroll
-        for (int s = 0; s < D / 16; ++s) {
-          const u32x4_t a = *(const u32x4_t *)(ks + k_rd + 32 * kb * C::RK + 32 * s);
-          sacc[kb] = mfma32x32x16<BF16>(a, qf[s], sacc[kb]);
-        }
-      }
-
-      // Mask only tiles crossing the diagonal or the ragged key tail.
-      const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && kbase + BN - 1 > q0w);
-      if (need_mask) {
-        // Register r of block kb holds key kbase + 4h + (32kb + 8(r>>2) + (r&3));
-        // it is visible iff that offset <= lim.
-        const int last_key = CAUSAL ? min(qrow, p.Sk - 1) : p.Sk - 1;
-        const int lim = last_key - kbase - 4 * h;
-#pragma unroll
-        for (int kb = 0; kb < BN / 32; ++kb) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int off = 32 * kb + 8 * (r >> 2) + (r & 3);
-            sacc[kb][r] = off <= lim ? sacc[kb][r] : -INFINITY;
-          }
-        }
-      }
-
-      // Online softmax for this lane's query.
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < BN / 32; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
-      mx = halves_max(mx);
-      const float m_cand = mx * c;
-      const bool upd = m_cand > m_run + kLazyMaxThreshold;
-      const float m_new = upd ? m_cand : m_run;
-      if (__builtin_amdgcn_ballot_w64(upd)) {
-        const float alpha = upd ? fast_exp2(m_run - m_new) : 1.f;
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < D / 32; ++db) oacc[db] *= alpha;
-      }
-      m_run = m_new;
-      const float mb = (m_new == -INFINITY) ? 0.f : m_new;
-
-      float lsum[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb = 0; kb < BN / 32; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pv = fast_exp2(__builtin_fmaf(sacc[kb][r], c, -mb));
-          sacc[kb][r] = pv;
-          lsum[r & 3] += pv;
-        }
-      l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
-
-      // P^T fragments: k-step ks (16 keys) = registers 8t..8t+7 of block ks/2.
-      u32x4_t pf[BN / 16];
-#pragma unroll
-      for (int ks2 = 0; ks2 < BN / 16; ++ks2) {
-        const int kb = ks2 >> 1, t8 = (ks2 & 1) * 8;
-        pf[ks2][0] = pack2<BF16>(sacc[kb][t8 + 0], sacc[kb][t8 + 1]);
-        pf[ks2][1] = pack2<BF16>(sacc[kb][t8 + 2], sacc[kb][t8 + 3]);
-        pf[ks2][2] = pack2<BF16>(sacc[kb][t8 + 4], sacc[kb][t8 + 5]);
-        pf[ks2][3] = pack2<BF16>(sacc[kb][t8 + 6], sacc[kb][t8 + 7]);
-      }
-
-      // O^T += V^T P^T: block db covers dims 32db .. +32.
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db) {
-        const int d = 32 * db + n;
-        const char *vrow = vs + d * C::RV;
-        const int sw = (d >> 3) & (C::NCH - 1);
-#pragma unroll
-        for (int ks2 = 0; ks2 < BN / 16; ++ks2) {
-          const u32x4_t a = *(const u32x4_t *)(vrow + (((2 * ks2 + h) ^ sw) * 16));
-          oacc[db] = mfma32x32x16<BF16>(a, pf[ks2], oacc[db]);
-        }
-      }
-    }
-
-    // Epilogue: normalise, store O rows and the natural-log LSE.  Rows >= Sq
-    // fall outside the buffer range and their stores are dropped.
-    const float l_tot = halves_sum(l_run);
-    const float inv = 1.f / l_tot;
-    {
-      const char *og = p.o + 2 * (bb * p.o_sb + hh * p.o_sh);
-      const BufRsrc ro = make_rsrc(og, (uint32_t)((int64_t)p.Sq * p.o_ss * 2));
-      const uint32_t oo = (uint32_t)(qrow * p.o_ss * 2 + 8 * h);
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          u32x2_t x;
-          x[0] = pack2<BF16>(oacc[db][4 * j + 0] * inv, oacc[db][4 * j + 1] * inv);
-          x[1] = pack2<BF16>(oacc[db][4 * j + 2] * inv, oacc[db][4 * j + 3] * inv);
-          buf_store8(x, ro, oo + 2 * (32 * db + 8 * j));
-        }
-    }
-    if (p.lse != nullptr) {
-      const uint32_t nbytes = (uint32_t)p.Sq * 4u;
-      const BufRsrc rl = make_rsrc(p.lse + ((int64_t)bb * p.H + hh) * p.Sq, nbytes);
-      const float lse = (m_run + __log2f(l_tot)) * kLn2;
-      buf_store4(__builtin_bit_cast(uint32_t, lse), rl, h ? nbytes : (uint32_t)qrow * 4u);
-    }
-    if (threadIdx.x == 0) s_ticket[(it + 1) & 1] = tq.finish(next_raw);
-    __syncthreads();  // LDS reuse by the next tile, ticket broadcast
-  }
-}
-
 // ---------------------------------------------------------------------------
-// Kernel v2: K and V tiles reach LDS by direct DMA (buffer_load ... lds), stay
+// Main kernel: K and V tiles reach LDS by direct DMA (buffer_load ... lds), stay
 // row-major there, and are read as MFMA operands with ds_read_b128 (K) and
 // the gfx950 transpose read ds_read_b64_tr_b16 (V^T), so no VGPR or VALU is
 // spent moving or transposing tiles.  NSTAGE LDS stages form a ring; tile
@@ -1180,7 +926,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Kernel v3 ("ping-pong"): 8 waves in two groups of 4.  Waves w and w + 4
+// Ping-pong kernel: 8 waves in two groups of 4.  Waves w and w + 4
 // share a SIMD.  Every wave runs the same action list
 //     M(0) S(0) M(1) S(1) ... M(n)
 // with  M(t) = O^T += V^T(t-1) P^T(t-1) and S^T(t) = K(t) Q^T  (32 MFMAs) and
@@ -1663,19 +1409,12 @@ typedef void (*KernelFn)(KernelArgs);
 
 struct KernelEntry {
   int32_t D, dtype, causal, BN, NW;
-  int32_t stages;     // LDS stages of the DMA kernel; 0 = register-staged kernel
+  int32_t stages;     // LDS stages in the K/V ring
   int32_t lds_bytes;
   int32_t wg_per_cu;  // resident workgroups per CU (registers and LDS)
   bool splittable;    // supports split-KV (partial outputs + merge)
   KernelFn fn;
 };
-
-template <int D, int BN, int NW, bool BF16, bool CAUSAL>
-constexpr KernelEntry entry() {
-  return KernelEntry{D, BF16 ? 1 : 0, CAUSAL ? 1 : 0, BN, NW, 0,
-                     FaConfig<D, BN, NW, BF16, CAUSAL>::LDS_BYTES, 8 / NW, false,
-                     fa_fwd_kernel<D, BN, NW, BF16, CAUSAL>};
-}
 
 template <int D, int BN, int NW, int NSTAGE, int OCC, bool BF16, bool CAUSAL, bool V8 = false>
 constexpr KernelEntry entry_dma() {
@@ -1684,9 +1423,6 @@ constexpr KernelEntry entry_dma() {
                      fa_fwd_dma_kernel<D, BN, NW, NSTAGE, OCC, BF16, CAUSAL, V8>};
 }
 
-#define FA_ENTRIES_DT_C(D, BN, NW)                                                   \
-  entry<D, BN, NW, false, false>(), entry<D, BN, NW, false, true>(),                 \
-      entry<D, BN, NW, true, false>(), entry<D, BN, NW, true, true>()
 #define FA_PP_ENTRIES(D, BN, NR)                                                                     \
   KernelEntry{D, 0, 0, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, false, fa_fwd_pp_kernel<D, BN, NR, false, false>}, \
   KernelEntry{D, 0, 1, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, false, fa_fwd_pp_kernel<D, BN, NR, false, true>},  \
@@ -1724,8 +1460,6 @@ const KernelEntry kKernels[] = {
     FA_DMA8_ENTRIES(256, 64, 4, 2, 1),
     FA_DMA8_ENTRIES(32, 64, 4, 2, 2),
     FA_DMA8_ENTRIES(16, 128, 4, 2, 2),
-    FA_ENTRIES_DT_C(64, 64, 4),
-    FA_ENTRIES_DT_C(128, 64, 4),
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 

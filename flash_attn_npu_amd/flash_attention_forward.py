@@ -40,7 +40,10 @@ DEFAULT_PERSISTENT_PROGRAMS = 0
 # 0 = the library's split-KV choice (fa_default_kv_splits: only grids that
 # would leave most workgroup slots empty); KV_SPLITS in [1, 64] overrides.
 DEFAULT_KV_SPLITS = 0
-PROFILE_OP_NAME = "fa_fwd_kernel"
+# Name prefix of the attention kernels in a profiler trace (fa_fwd_dma_kernel,
+# fa_fwd_pp_kernel); the reference names its Triton kernel here
+# (flash_attention_forward.py:25).
+PROFILE_OP_NAME = "fa_fwd"
 LIB_NAME = "libfa_mi355x.so"
 SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
 # The reference accepts these head dims (flash_attention_forward.py:1121-1122).
