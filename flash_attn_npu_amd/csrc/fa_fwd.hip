@@ -686,7 +686,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
         const int ks = i / C::DB, db = i % C::DB;
         const uint32_t imm = (uint32_t)(C::TILE + 16 * ks * C::ROW);
         const u32x2_t lo = lds_read_tr16(sbase, vro[db][0] + imm);
-        const u32x2_t hi = lds_read_tr16(sbase, vro[db][1] + imm + 8 * C::ROW);
+        const u32x2_t hi = lds_read_tr16(sbase, vro[db][V8 ? 0 : 1] + imm + 8 * C::ROW);
         u32x4_t f = {lo[0], lo[1], hi[0], hi[1]};
         if constexpr (D < 32) {
           if (lane & 16) f = (u32x4_t){0u, 0u, 0u, 0u};

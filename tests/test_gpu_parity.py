@@ -196,6 +196,26 @@ def test_persistent_grid(fa, monkeypatch):
         assert torch.equal(got, want) and torch.equal(got_lse, want_lse)
 
 
+def test_unequal_queues_and_slot_reuse(fa, monkeypatch):
+    """Queues of unequal length on a small grid: B*H = 9 heads over 8 queues
+    gives queue 0 twice the tiles of the others (2 workgroups per queue).
+    Every tile is computed exactly once (bit-identical to the full grid), and
+    the tile counters come back clean for the next launches, including after
+    every launch slot has been reused."""
+    g = torch.Generator().manual_seed(13)
+    q, k, v = (torch.randn((3, 3, 1024, 128), generator=g).to(torch.bfloat16).cuda() for _ in range(3))
+    want, want_lse = fa.attention(q, k, v, True, 0.1, return_lse=True)
+    monkeypatch.setenv("PERSISTENT_PROGRAMS", "16")
+    assert fa._describe_runtime(3, 3, 1024, 128, True)["launched_programs"] == 16
+    for i in range(1100):  # more launches than the library has queue slots (1024)
+        got, got_lse = fa.attention(q, k, v, True, 0.1, return_lse=True)
+        if i % 100 == 0 or i == 1099:
+            assert torch.equal(got, want) and torch.equal(got_lse, want_lse), f"launch {i}"
+    monkeypatch.delenv("PERSISTENT_PROGRAMS")
+    got, got_lse = fa.attention(q, k, v, True, 0.1, return_lse=True)
+    assert torch.equal(got, want) and torch.equal(got_lse, want_lse)
+
+
 def test_deterministic(fa):
     w = W.CONFIGS[0]
     q, k, v = W.make_inputs(w, device="cuda")
