@@ -1555,6 +1555,21 @@ unsigned long long *queue_base(int device) {
   return ptr;
 }
 
+// CU count per device, asked once (the attribute query costs about a
+// microsecond, a sizeable part of a launch).
+std::atomic<int> g_cu_count[kMaxDevices];
+
+int device_cu_count(int device) {
+  if (device < 0 || device >= kMaxDevices) return kDefaultCuCount;
+  int n = g_cu_count[device].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n <= 0)
+      n = kDefaultCuCount;
+    g_cu_count[device].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 }  // namespace
@@ -1580,10 +1595,8 @@ int launch(const fa_fwd_params *p, void *hip_stream, int splits, void *workspace
   const int rc = fa_validate(p);
   if (rc != FA_OK) return rc;
   if (p->B == 0 || p->H == 0 || p->Sq == 0) return FA_OK;
-  int device = 0, cu_count = 0;
-  if (hipGetDevice(&device) != hipSuccess ||
-      hipDeviceGetAttribute(&cu_count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
-    cu_count = kDefaultCuCount;
+  int device = 0;
+  const int cu_count = hipGetDevice(&device) == hipSuccess ? device_cu_count(device) : kDefaultCuCount;
   Plan plan;
   const int prc = make_plan(p, &plan, cu_count, splits);
   if (prc != FA_OK) return prc;

@@ -231,13 +231,21 @@ def _query_config(z, h, n_ctx, head_dim, causal, bm=0, bn=0, dtype=torch.float16
     return list(out)
 
 
+# The library's default tiling is a pure function of the shape: asked once per shape.
+_FALLBACK_TILING = {}
+
+
 def _default_tiling(z, h, n_ctx, head_dim, causal):
     """Preset for this exact shape, else the library's gfx950 default."""
-    preset = DEFAULT_TILING_PRESETS.get((z, h, n_ctx, head_dim, causal))
+    key = (z, h, n_ctx, head_dim, causal)
+    preset = DEFAULT_TILING_PRESETS.get(key)
     if preset is not None:
         return preset
-    cfg = _query_config(z, h, n_ctx, head_dim, causal)
-    return cfg[0], cfg[1]
+    tiling = _FALLBACK_TILING.get(key)
+    if tiling is None:
+        cfg = _query_config(z, h, n_ctx, head_dim, causal)
+        tiling = _FALLBACK_TILING[key] = (cfg[0], cfg[1])
+    return tiling
 
 
 def get_tiling(z, h, n_ctx, head_dim, causal):
@@ -306,6 +314,8 @@ def _validate_inputs(q, k, v):
 
 def _kernel_ready(t):
     """A view the kernel can read directly: dim stride 1, 16-byte rows, 16B-aligned."""
+    if t.is_contiguous() and t.data_ptr() % 16 == 0:
+        return t  # rows of D >= 16 elements: every stride is a multiple of 16 bytes
     st = t.stride()
     align = 16 // t.element_size()
     if st[3] != 1 or any(s % align for s in st[:3]) or t.data_ptr() % 16:
@@ -313,11 +323,6 @@ def _kernel_ready(t):
     if t.shape[2] > 1 and st[2] < t.shape[3]:
         return t.contiguous()
     return t
-
-
-def _fill_strides(arr, t):
-    for i, s in enumerate(t.stride()):
-        arr[i] = s
 
 
 def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
@@ -344,30 +349,47 @@ def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
     lib = _load_library()
     p = FaFwdParams()
     p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
-    _fill_strides(p.q_stride, q)
-    _fill_strides(p.k_stride, k)
-    _fill_strides(p.v_stride, v)
-    _fill_strides(p.o_stride, out)
+    p.q_stride[:] = q.stride()
+    p.k_stride[:] = k.stride()
+    p.v_stride[:] = v.stride()
+    p.o_stride[:] = out.stride()
     p.B, p.H, p.Sq, p.Sk, p.D = z, h, n_ctx, n_ctx, head_dim
     p.dtype = FA_DTYPE[q.dtype] + (FA_DTYPE_V_E5M2_OFFSET if fp8_v else 0)
     p.causal = 1 if causal else 0
     p.sm_scale = sm_scale
     p.block_m, p.block_n = int(bm), int(bn)
     p.num_programs = _get_persistent_programs()
+    pp = ctypes.byref(p)
     splits = _get_kv_splits()
     if splits == 0:
-        splits = int(lib.fa_default_kv_splits(ctypes.byref(p)))
-    with torch.cuda.device(q.device):
-        stream = torch.cuda.current_stream(q.device).cuda_stream
-        if splits > 1:
-            nbytes = int(lib.fa_split_workspace_bytes(ctypes.byref(p), splits))
-            _check(nbytes if nbytes < 0 else 0, "fa_split_workspace_bytes")
-            workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device)  # caching allocator: 512 B aligned
-            _check(lib.fa_fwd_split(ctypes.byref(p), splits, ctypes.c_void_p(workspace.data_ptr()), nbytes,
-                                    ctypes.c_void_p(stream)), "fa_fwd_split")
-        else:
-            _check(lib.fa_fwd(ctypes.byref(p), ctypes.c_void_p(stream)), "fa_fwd")
+        splits = int(lib.fa_default_kv_splits(pp))
+    dev = q.device.index
+    if dev == torch.cuda.current_device():
+        _launch_on(lib, pp, splits, dev, q.device)
+    else:
+        with torch.cuda.device(dev):
+            _launch_on(lib, pp, splits, dev, q.device)
     return out, lse
+
+
+def _launch_on(lib, pp, splits, dev, device):
+    """Launch on the current stream of device `dev` (the current device)."""
+    stream = _current_raw_stream(dev)
+    if splits > 1:
+        nbytes = int(lib.fa_split_workspace_bytes(pp, splits))
+        _check(nbytes if nbytes < 0 else 0, "fa_split_workspace_bytes")
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)  # caching allocator: 512 B aligned
+        _check(lib.fa_fwd_split(pp, splits, workspace.data_ptr(), nbytes, stream), "fa_fwd_split")
+    else:
+        _check(lib.fa_fwd(pp, stream), "fa_fwd")
+
+
+def _current_raw_stream(dev):
+    """hipStream_t of torch's current stream on device `dev`, as an int."""
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        return raw(dev)
+    return torch.cuda.current_stream(dev).cuda_stream
 
 
 def attention(q, k, v, causal, sm_scale, BM=None, BN=None, return_lse=False):
