@@ -427,6 +427,13 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(OC
 fa_fwd_dma_kernel(KernelArgs p) {
   using C = Cfg2<D, BN, NW, NSTAGE, OCC, V8>;
   constexpr int ESV = V8 ? 1 : 2;  // bytes per V element
+  // fp16 at D = 16, where the softmax VALU work dwarfs the 12 MFMAs of a
+  // tile: the row sum moves from BN VALU adds per tile to BN / 16 MFMAs over
+  // the fp16 P (relative change of l at most 2^-11, the fp16 rounding of p;
+  // bf16 would allow 2^-9, too close to the LSE tolerance).  Measured 5.6%
+  // faster at D = 16; at D = 32 equal and at D = 64 1.3-1.8% slower, where
+  // the extra MFMA time costs what the adds saved.
+  constexpr bool MSUM = !BF16 && !V8 && D == 16;
   constexpr int BM = C::BM;
   // One array per stage: the compiler's LDS-DMA alias tracking then knows
   // that DMAs into one stage never feed reads of the other, and adds no
@@ -597,6 +604,12 @@ fa_fwd_dma_kernel(KernelArgs p) {
     for (int db = 0; db < C::DB; ++db) oacc[db] = (f32x16_t){};
     float m_run = -INFINITY;
     float l_run = 0.f;
+    // MSUM: the row sum l on the matrix core, as one more O^T block whose
+    // A operand is 1 in rows 0 and 4 (lane halves' element 0) and 0 elsewhere:
+    // l = sum of the fp16 P fed to P.V, in fp32.
+    f32x16_t lacc = {};
+    const uint32_t one2 = ((lane & 31) == 0 || (lane & 31) == 4) ? 0x3C003C00u : 0u;  // fp16 (1, 1)
+    const u32x4_t ones = {one2, one2, one2, one2};
 
     // One KV tile: wait for its DMA, barrier, refill the other stage, then
     // S^T = K Q^T, online softmax, O^T += V^T P^T.  MASKED is a compile-time
@@ -758,7 +771,10 @@ fa_fwd_dma_kernel(KernelArgs p) {
       const float m_new = upd ? m_cand : m_run;
       if (__builtin_amdgcn_ballot_w64(upd)) {
         const float alpha = upd ? fast_exp2(m_run - m_new) : 1.f;
-        l_run *= alpha;
+        if constexpr (MSUM)
+          lacc[0] *= alpha;
+        else
+          l_run *= alpha;
 #pragma unroll
         for (int db = 0; db < C::DB; ++db) oacc[db] *= alpha;
       }
@@ -812,7 +828,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) pf[ks][w] = pack2<BF16>(sacc[kb][t8 + 2 * w], sacc[kb][t8 + 2 * w + 1]);
       }
-      l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+      if constexpr (!MSUM) l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
 
       // O^T += V^T P^T; the A operand is two transpose reads (keys +0..3 and
       // +8..11 of the k-step), VPF fragments ahead of their MFMA.  For
@@ -828,12 +844,16 @@ fa_fwd_dma_kernel(KernelArgs p) {
         const int ks = i / C::DB, db = i % C::DB;
         oacc[db] = mfma32x32x16<BF16>(vfr[i], pf[ks], oacc[db]);
       }
+      if constexpr (MSUM) {
+#pragma unroll
+        for (int ks = 0; ks < BN / 16; ++ks) lacc = mfma32x32x16<BF16>(ones, pf[ks], lacc);
+      }
 #pragma unroll
       for (int i = 0; i < NPV - VPF; ++i) {
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
         __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, VPF, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, VPF + (MSUM ? BN / 16 : 0), 0);
       if constexpr (D >= 128) __builtin_amdgcn_s_setprio(0);
       }
     };
@@ -860,7 +880,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
     tm_epi0 = FA_CLK() - tm0;
 #endif
 
-    const float l_tot = halves_sum(l_run);
+    const float l_tot = MSUM ? lacc[0] : halves_sum(l_run);
     if (p.kv_splits > 1) {
       // Partial result of this KV run: O normalised by its own row sum, in
       // fp32, and its natural-log LSE (-inf, with O = 0, where no key of the
