@@ -242,6 +242,32 @@ def test_tiling_resolution(monkeypatch):
     assert fa.get_tiling_source(2, 3, 4097, 128, True) == "fallback"
 
 
+def test_fallback_tiling_cached_per_shape(monkeypatch):
+    """The library's default tiling is asked once per shape and the cached
+    answer is the library's; a preset for the shape still wins."""
+    key = (3, 5, 777, 64, True)
+    fa._FALLBACK_TILING.pop(key, None)
+    want = tuple(fa._query_config(*key)[:2])
+    calls = []
+    real = fa._query_config
+    monkeypatch.setattr(fa, "_query_config", lambda *a, **k: calls.append(a) or real(*a, **k))
+    assert fa.get_tiling(*key) == want
+    assert fa.get_tiling(*key) == want
+    assert len(calls) == 1
+    monkeypatch.setitem(fa.DEFAULT_TILING_PRESETS, key, (128, 32))
+    assert fa.get_tiling(*key) == (128, 32)
+
+
+def test_kernel_ready_fast_path_and_copies():
+    t = torch.zeros((2, 3, 40, 64), dtype=torch.float16)
+    assert fa._kernel_ready(t) is t  # contiguous, 16-byte aligned: read in place
+    view = t.permute(0, 2, 1, 3)  # [B, S, H, D] strides: still readable in place
+    assert fa._kernel_ready(view) is view
+    odd = torch.zeros((1, 2, 40, 72), dtype=torch.float16)[..., 1:65]  # misaligned base
+    ready = fa._kernel_ready(odd)
+    assert ready is not odd and ready.is_contiguous() and torch.equal(ready, odd)
+
+
 def test_persistent_programs_env(monkeypatch):
     monkeypatch.delenv("PERSISTENT_PROGRAMS", raising=False)
     assert fa._get_persistent_programs() == fa.DEFAULT_PERSISTENT_PROGRAMS
