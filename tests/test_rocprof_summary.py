@@ -1,0 +1,101 @@
+"""CPU: the rocprofv3 pass summarizer and the profile_summary.{json,txt} writer.
+
+The summary must carry every key the reference's comparison tool reads
+(compare_results_plus.py:283-338 for an entry, :447-479 for the printed
+comparison), so two MI355X runs compare with that tool unmodified, and the
+HBM byte figures must be scaled by the plain-copy calibration that runs in
+the same process.
+"""
+
+from __future__ import annotations
+
+import csv
+import json
+
+import pytest
+
+from flash_attn_npu_amd import rocprof
+
+KERNEL = "void (anonymous namespace)::fa_fwd_dma_kernel<128, 64, 4, 2, 2, true, true, false>(KernelArgs)"
+COPY = "void at::native::elementwise_kernel<copy>(...)"
+
+
+def _write_trace(path, rows):
+    with path.open("w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Kernel_Name", "Start_Timestamp", "End_Timestamp", "Grid_Size_X",
+                                          "Workgroup_Size_X", "LDS_Block_Size", "VGPR_Count", "Scratch_Size"])
+        w.writeheader()
+        for name, start_ns, dur_ns in rows:
+            w.writerow({"Kernel_Name": name, "Start_Timestamp": start_ns, "End_Timestamp": start_ns + dur_ns,
+                        "Grid_Size_X": 512 * 256, "Workgroup_Size_X": 256, "LDS_Block_Size": 66048,
+                        "VGPR_Count": 128, "Scratch_Size": 12})
+
+
+def _write_counters(path, rows):
+    with path.open("w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Kernel_Name", "Counter_Name", "Counter_Value"])
+        w.writeheader()
+        for name, counter, value in rows:
+            w.writerow({"Kernel_Name": name, "Counter_Name": counter, "Counter_Value": value})
+
+
+@pytest.fixture()
+def passes(tmp_path):
+    trace = tmp_path / "KernelTrace" / "host"
+    trace.mkdir(parents=True)
+    # Three attention launches (150, 152, 154 us) and one 50 us copy.
+    _write_trace(trace / "run_kernel_trace.csv",
+                 [(KERNEL, 0, 150_000), (KERNEL, 200_000, 152_000), (KERNEL, 400_000, 154_000), (COPY, 600_000, 50_000)])
+    read = tmp_path / "HBMRead" / "host"
+    read.mkdir(parents=True)
+    # The 256 MiB copy reads as 96 MiB (factor 8/3); the kernel reads 190,000 KiB per launch.
+    _write_counters(read / "run_counter_collection.csv",
+                    [(KERNEL, "FETCH_SIZE", 190_000.0), (KERNEL, "FETCH_SIZE", 190_000.0),
+                     (COPY, "FETCH_SIZE", 96 * 1024.0)])
+    l2 = tmp_path / "L2" / "host"
+    l2.mkdir(parents=True)
+    _write_counters(l2 / "run_counter_collection.csv",
+                    [(KERNEL, "TCC_HIT_sum", 740.0), (KERNEL, "TCC_MISS_sum", 260.0)])
+    return tmp_path
+
+
+def test_kernel_trace_pass(passes):
+    e = rocprof.summarize_pass(passes / "KernelTrace")
+    op = e["op"]
+    assert op["OP Type"] == KERNEL and op["Count"] == 3.0
+    assert op["Avg Time(us)"] == pytest.approx(152.0) and op["Min Time(us)"] == pytest.approx(150.0)
+    assert op["Max Time(us)"] == pytest.approx(154.0) and op["Total Time(us)"] == pytest.approx(456.0)
+    assert op["Ratio(%)"] == pytest.approx(100.0 * 456.0 / 506.0)  # the copy is not the target op
+    assert e["kernel"]["kernel_count"] == 3.0 and e["kernel"]["Block Num"] == 512.0
+    assert e["kernel"]["Duration(us)"] == pytest.approx(152.0)
+
+
+def test_fetch_scaled_by_copy_calibration(passes):
+    k = rocprof.summarize_pass(passes / "HBMRead")["kernel"]
+    factor = rocprof.COPY_BYTES / (96 * 1024.0 * 1024.0)
+    assert k["FETCH_SIZE_copy_factor"] == pytest.approx(factor) == pytest.approx(8 / 3)
+    assert k["hbm_read_bytes"] == pytest.approx(190_000.0 * 1024.0 * factor)
+
+
+def test_l2_hit_rate(passes):
+    e = rocprof.summarize_pass(passes / "L2")
+    assert e["l2"]["Hit Rate"] == pytest.approx(0.74) and e["l2_columns"] == ["Hit Rate"]
+
+
+def test_summary_files_carry_the_comparison_tool_keys(passes):
+    summary = rocprof.summarize_dir(passes, plan={"KernelTrace": None, "HBMRead": ["FETCH_SIZE"], "L2": ["x"]})
+    j, t = rocprof.write_profile_summary_files(passes / "out", summary)
+    data = json.loads(j.read_text())
+    assert set(data) == {"KernelTrace", "HBMRead", "L2"}
+    for entry in data.values():
+        # Keys read per entry by compare_results_plus.py:319-338 and printed at :447-479.
+        assert {"profiler_output", "op_name", "op", "kernel", "kernel_columns", "step", "api", "l2",
+                "l2_columns"} <= set(entry)
+        assert isinstance(entry["kernel_columns"], list) and isinstance(entry["l2_columns"], list)
+        for c in entry["kernel_columns"]:
+            assert c in entry["kernel"]
+    op = data["KernelTrace"]["op"]
+    for key in ("OP Type", "Count", "Total Time(us)", "Min Time(us)", "Avg Time(us)", "Max Time(us)", "Ratio(%)"):
+        assert key in op
+    text = t.read_text()
+    assert "[KernelTrace]" in text and "avg_us=152.000" in text and "Hit Rate=0.740000" in text
