@@ -874,8 +874,28 @@ fa_fwd_dma_kernel(KernelArgs p) {
       }
       if (t < end) kv_tile(t++, masked_tag, S0{});
     };
-    run(n_full, std::integral_constant<bool, false>{});
-    run(n_tiles, std::integral_constant<bool, true>{});
+    if (OCC == 2 && q0w >= p.Sq) {
+      // No row of this wave is in range (the ragged last m-tile): when
+      // another workgroup's wave shares the SIMD, only keep the DMA ring and
+      // the barriers in step with the other waves.  Its stores then fall
+      // past the buffers' ranges and are dropped.
+      for (; t < n_tiles; ++t) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __syncthreads();
+        BufRsrc rk_n, rv_n;
+        tile_rsrc(t + 1, &rk_n, &rv_n);
+        if (t & 1) {
+#pragma unroll
+          for (int i = 0; i < C::NDMA; ++i) dma(S0{}, rk_n, rv_n, i);
+        } else {
+#pragma unroll
+          for (int i = 0; i < C::NDMA; ++i) dma(S1{}, rk_n, rv_n, i);
+        }
+      }
+    } else {
+      run(n_full, std::integral_constant<bool, false>{});
+      run(n_tiles, std::integral_constant<bool, true>{});
+    }
 #ifdef FA_TIMING
     tm_epi0 = FA_CLK() - tm0;
 #endif
