@@ -415,7 +415,7 @@ struct Cfg2 {
   static_assert(!V8 || (BN % 64 == 0 && (D >= 32 ? BN == 64 : BN == 128)), "fp8 V: 64-key tiles (D = 16: 128)");
   static_assert(BN % 32 == 0, "tile shape");
   static_assert(NSTAGE == 2, "double-buffered: one tile computes while the next lands");
-  static_assert(OCC == 1 || OCC == 2, "workgroups per CU");
+  static_assert(OCC >= 1 && OCC <= 4, "workgroups per CU");
   static_assert(LDS_BYTES * OCC <= 160 * 1024, "LDS budget of one gfx950 CU");
 };
 
@@ -647,13 +647,13 @@ fa_fwd_dma_kernel(KernelArgs p) {
 #endif
 
       // A wave whose rows all precede this causal tile only issues its DMAs
-      // when another workgroup's wave shares its SIMD (OCC = 2).  With one
+      // when another workgroup's wave shares its SIMD (OCC >= 2).  With one
       // workgroup per CU it computes the tile fully masked (p = 0) instead:
       // the workgroup waits for its last wave either way, and the early exit
       // cost the D = 256 kernels ~100 registers and scratch spills (masked
       // tiles were ~10x slower).
       const int kbase = t * BN;
-      if (MASKED && CAUSAL && OCC == 2 && kbase > wave_last_q) {
+      if (MASKED && CAUSAL && OCC >= 2 && kbase > wave_last_q) {
 #pragma unroll
         for (int i = 0; i < NDMA; ++i) dma(NEXT{}, rk_n, rv_n, i);
 #ifdef FA_TIMING
@@ -874,7 +874,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
       }
       if (t < end) kv_tile(t++, masked_tag, S0{});
     };
-    if (OCC == 2 && q0w >= p.Sq) {
+    if (OCC >= 2 && q0w >= p.Sq) {
       // No row of this wave is in range (the ragged last m-tile): when
       // another workgroup's wave shares the SIMD, only keep the DMA ring and
       // the barriers in step with the other waves.  Its stores then fall
@@ -1482,19 +1482,25 @@ const KernelEntry kKernels[] = {
     FA_DMA_ENTRIES(128, 64, 4, 2, 2),
     FA_PP_ENTRIES(128, 64, 4),
     FA_DMA_ENTRIES(128, 32, 4, 2, 2),
-    FA_DMA_ENTRIES(64, 64, 4, 2, 2),
+    // D <= 64 is softmax (VALU) bound, and a single wave issues VALU work
+    // well below the SIMD's rate: more resident waves fill the gaps.  D = 64
+    // default: 64-key tiles, whose 32 KB of LDS and <= 168 registers let three
+    // workgroups share a CU (0.7-7.7% faster than 128-key tiles at two, on
+    // every D = 64 workload measured, fp16 and bf16, causal and not).
+    FA_DMA_ENTRIES(64, 64, 4, 2, 3),
     FA_PP_ENTRIES(64, 64, 4),
     FA_DMA_ENTRIES(64, 32, 4, 2, 2),
-    // D = 64 default: 128-key tiles halve the per-tile barrier, DMA issue and
-    // loop overhead per key (1.5-4% over 64-key tiles on every D = 64 workload
-    // measured, fp16 and bf16, causal and not).
     FA_DMA_ENTRIES(64, 128, 4, 2, 2),
     // D = 256: 512 registers per wave (O^T alone is 128), so one workgroup
     // per CU; 32-key tiles keep S, P and the operand fragments small.
     FA_DMA_ENTRIES(256, 32, 4, 2, 1),
-    FA_DMA_ENTRIES(32, 64, 4, 2, 2),
-    // D = 16: a 64-key tile is only two DMA instructions; 128 keys give each wave one.
-    FA_DMA_ENTRIES(16, 128, 4, 2, 2),
+    // D = 32: four workgroups per CU when causal (8-9% faster than two);
+    // non-causal measured 1.7% slower at four, so it keeps two.
+    entry_dma<32, 64, 4, 2, 2, false, false>(), entry_dma<32, 64, 4, 2, 4, false, true>(),
+    entry_dma<32, 64, 4, 2, 2, true, false>(), entry_dma<32, 64, 4, 2, 4, true, true>(),
+    // D = 16: a 64-key tile is only two DMA instructions; 128 keys give each
+    // wave one.  Three workgroups per CU (4-10% faster than two).
+    FA_DMA_ENTRIES(16, 128, 4, 2, 3),
     FA_DMA8_ENTRIES(128, 64, 4, 2, 2),
     FA_DMA8_ENTRIES(64, 64, 4, 2, 2),
     FA_DMA8_ENTRIES(256, 64, 4, 2, 1),
@@ -1518,7 +1524,7 @@ void default_tiling(int D, int dtype, int causal, int *bn, int *nw) {
   (void)causal;
   // fp8 V: 64-key tiles (D = 16: 128), one 32x32x64 MFMA per 64 keys and 32
   // head dims.
-  *bn = v_is_fp8(dtype) ? (D == 16 ? 128 : 64) : ((D == 16 || D == 64) ? 128 : (D == 256 ? 32 : 64));
+  *bn = v_is_fp8(dtype) ? (D == 16 ? 128 : 64) : (D == 16 ? 128 : (D == 256 ? 32 : 64));
   *nw = 4;
 }
 
@@ -1843,7 +1849,10 @@ int32_t fa_default_kv_splits(const fa_fwd_params *p) {
   if (!e.splittable) return 1;
   // Split only a grid that would leave most workgroup slots empty, and only
   // into runs of at least 8 KV tiles (the merge costs an extra HBM pass).
-  const int64_t slots = (int64_t)e.wg_per_cu * kDefaultCuCount;
+  // Slots count at most two workgroups per CU: a third or fourth one only
+  // fills VALU issue gaps, and splitting further to occupy it cost more in
+  // merge work (B2 H4 S4096 D16 causal: 3 splits 8% slower than 2).
+  const int64_t slots = (int64_t)(e.wg_per_cu < 2 ? e.wg_per_cu : 2) * kDefaultCuCount;
   if (plan.total_tiles * 2 > slots) return 1;
   const int64_t kv_tiles = ((int64_t)p->Sk + plan.BN - 1) / plan.BN;
   int64_t splits = (slots + plan.total_tiles - 1) / plan.total_tiles;
