@@ -1502,10 +1502,12 @@ const KernelEntry kKernels[] = {
     // wave one.  Three workgroups per CU (4-10% faster than two).
     FA_DMA_ENTRIES(16, 128, 4, 2, 3),
     FA_DMA8_ENTRIES(128, 64, 4, 2, 2),
-    FA_DMA8_ENTRIES(64, 64, 4, 2, 2),
+    // fp8 V at D <= 64: three workgroups per CU (causal 6.7-8.4% faster than
+    // two, non-causal equal).
+    FA_DMA8_ENTRIES(64, 64, 4, 2, 3),
     FA_DMA8_ENTRIES(256, 64, 4, 2, 1),
-    FA_DMA8_ENTRIES(32, 64, 4, 2, 2),
-    FA_DMA8_ENTRIES(16, 128, 4, 2, 2),
+    FA_DMA8_ENTRIES(32, 64, 4, 2, 3),
+    FA_DMA8_ENTRIES(16, 128, 4, 2, 3),
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
