@@ -34,6 +34,9 @@
 //    waves skip tiles above their own diagonal, and only tiles crossing the
 //    diagonal or the ragged key tail evaluate the mask.  Ragged query/key
 //    tails are zero-filled on load, masked to -inf, and never stored.
+//  * Workgroups per CU: 2 at D = 128, 1 at D = 256, 3 or 4 at D <= 64, where
+//    the softmax VALU work outweighs the MFMAs and more resident waves fill
+//    the VALU issue gaps a single wave leaves.
 //  * Grid: persistent (as many workgroups as are resident at once); the
 //    workgroups of each XCD pull (head, m-tile) tiles, heaviest first, from
 //    a tile queue that owns a fixed set of heads, so a head's K/V is read
@@ -192,9 +195,9 @@ __device__ __forceinline__ int vt_pos(int k) {
 // so a head's K/V is only ever read through one XCD's L2.  A queue hands out
 // its tiles heaviest first (causal: largest m-tile first, across its heads),
 // so the tail is made of the cheapest tiles.  Pulling instead of a static
-// split matters on gfx950: the two workgroups sharing a CU do not progress
-// at the same rate (the older one wins issue arbitration), so any fixed
-// assignment leaves one of them idle at the end.
+// split matters on gfx950: workgroups sharing a CU do not progress at the
+// same rate (the older one wins issue arbitration), so any fixed assignment
+// leaves some of them idle at the end.
 //
 // Ticket i of a queue is its i-th heaviest tile.  The queue's W workgroups
 // take tickets 0..W-1 statically (no atomic before the first tile); later
