@@ -28,7 +28,7 @@ def _inputs(seed, shape, dtype):
 
 
 @pytest.mark.parametrize("splits", [2, 3, 7, 64])
-@pytest.mark.parametrize("d", [16, 64, 128, 256])
+@pytest.mark.parametrize("d", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 def test_forced_splits_vs_fp64(fa, monkeypatch, splits, d, causal):
     dtype = torch.bfloat16 if d in (128, 256) else torch.float16
