@@ -244,6 +244,33 @@ def test_lse_null_through_c_abi(fa):
     assert torch.equal(out, want)
 
 
+@pytest.mark.parametrize("sq,sk", [(100, 333), (333, 100), (1, 700), (700, 1), (256, 4096), (3000, 129)])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("d,dtype", [(64, torch.float16), (128, torch.bfloat16), (32, torch.bfloat16)],
+                         ids=["d64-fp16", "d128-bf16", "d32-bf16"])
+def test_rectangular_sq_sk_through_c_abi(fa, sq, sk, causal, d, dtype):
+    """Sq != Sk through the C ABI (the reference requires Sq == Sk; the kernel
+    does not): causal is top-left aligned, key j visible to query i iff j <= i,
+    so rows past Sk see every key and keys past Sq are never seen."""
+    import ctypes
+    _say(f"[rect] Sq={sq} Sk={sk} D={d} {DT_NAME[dtype]} causal={causal}")
+    lib = fa._load_library()
+    g = torch.Generator().manual_seed(sq * 7 + sk + d)
+    q = torch.randn((2, 3, sq, d), generator=g).to(dtype).cuda()
+    k, v = (torch.randn((2, 3, sk, d), generator=g).to(dtype).cuda() for _ in range(2))
+    out = torch.empty_like(q)
+    lse = torch.empty((2, 3, sq), dtype=torch.float32, device="cuda")
+    p = fa.FaFwdParams()
+    p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
+    p.q_stride[:], p.k_stride[:], p.v_stride[:], p.o_stride[:] = q.stride(), k.stride(), v.stride(), out.stride()
+    p.B, p.H, p.Sq, p.Sk, p.D = 2, 3, sq, sk, d
+    p.dtype, p.causal, p.sm_scale = fa.FA_DTYPE[dtype], int(causal), d ** -0.5
+    assert lib.fa_fwd(ctypes.byref(p), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)) == 0
+    o64, l64 = attention_fp64(q, k, v, causal, d ** -0.5)
+    assert (out.float() - o64.to(dtype).float()).abs().max().item() <= O_TOL[dtype]
+    assert (lse.double() - l64).abs().max().item() <= LSE_TOL
+
+
 def test_empty_batch(fa):
     q = torch.empty((0, 4, 128, 64), dtype=torch.float16, device="cuda")
     out, lse = fa.attention(q, q, q, True, 0.1, return_lse=True)
