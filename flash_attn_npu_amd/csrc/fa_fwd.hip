@@ -1743,7 +1743,7 @@ const char *fa_error_string(int code) {
     case FA_OK: return "ok";
     case FA_ERR_NULL: return "a required tensor pointer is NULL";
     case FA_ERR_SHAPE: return "invalid shape (negative size, Sq>0 with Sk==0, or too many tiles)";
-    case FA_ERR_HEAD_DIM: return "HEAD_DIM is not supported by this build";
+    case FA_ERR_HEAD_DIM: return "HEAD_DIM is not one of 16, 32, 64, 128, 256";
     case FA_ERR_DTYPE: return "dtype must be fp16 or bf16 (optionally with fp8-e5m2 V)";
     case FA_ERR_STRIDE: return "the head-dim stride must be 1 and the other strides multiples of 8 elements (16 for an fp8 V)";
     case FA_ERR_ALIGN: return "tensor base pointers must be 16-byte aligned";

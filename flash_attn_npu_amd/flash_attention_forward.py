@@ -302,7 +302,7 @@ def _validate_inputs(q, k, v):
     if q.shape[-1] not in REFERENCE_HEAD_DIMS:
         raise ValueError("HEAD_DIM must be one of {16, 32, 64, 128, 256}")
     if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
-        raise ValueError(f"HEAD_DIM={q.shape[-1]} is not supported by this build "
+        raise ValueError(f"HEAD_DIM={q.shape[-1]} is not supported by this library "
                          f"(supported: {SUPPORTED_HEAD_DIMS})")
     if q.dtype not in FA_DTYPE or k.dtype != q.dtype or (v.dtype != q.dtype and v.dtype != FP8_V_DTYPE):
         raise ValueError("q, k, v must all be float16 or all be bfloat16 (v may also be float8_e5m2)")
