@@ -649,21 +649,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
       tm_dma += td - tc;
 #endif
 
-      // A wave whose rows all precede this causal tile only issues its DMAs
-      // when another workgroup's wave shares its SIMD (OCC >= 2).  With one
-      // workgroup per CU it computes the tile fully masked (p = 0) instead:
-      // the workgroup waits for its last wave either way, and the early exit
-      // cost the D = 256 kernels ~100 registers and scratch spills (masked
-      // tiles were ~10x slower).
       const int kbase = t * BN;
-      if (MASKED && CAUSAL && OCC >= 2 && kbase > wave_last_q) {
-#pragma unroll
-        for (int i = 0; i < NDMA; ++i) dma(NEXT{}, rk_n, rv_n, i);
-#ifdef FA_TIMING
-        tm_idle += 1;
-#endif
-        return;
-      }
 #ifdef FA_TIMING
       ++n_comp;
       struct Stamp {
@@ -877,12 +863,11 @@ fa_fwd_dma_kernel(KernelArgs p) {
       }
       if (t < end) kv_tile(t++, masked_tag, S0{});
     };
-    if (OCC >= 2 && q0w >= p.Sq) {
-      // No row of this wave is in range (the ragged last m-tile): when
-      // another workgroup's wave shares the SIMD, only keep the DMA ring and
-      // the barriers in step with the other waves.  Its stores then fall
-      // past the buffers' ranges and are dropped.
-      for (; t < n_tiles; ++t) {
+    // Tiles [t, end) in which this wave has nothing to compute: only keep the
+    // DMA ring and the barriers in step with the other waves (one barrier
+    // per tile, like kv_tile).
+    auto idle_tiles = [&](int end) __attribute__((always_inline)) {
+      for (; t < end; ++t) {
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __syncthreads();
         BufRsrc rk_n, rv_n;
@@ -894,10 +879,27 @@ fa_fwd_dma_kernel(KernelArgs p) {
 #pragma unroll
           for (int i = 0; i < C::NDMA; ++i) dma(S1{}, rk_n, rv_n, i);
         }
+#ifdef FA_TIMING
+        tm_idle += 1;
+#endif
       }
+    };
+    // When another workgroup's wave shares the SIMD (OCC >= 2), a wave skips
+    // the tiles it has no work in: all of them when none of its rows is in
+    // range (the ragged last m-tile; its stores then fall past the buffers'
+    // ranges and are dropped), and under the causal mask the tiles past its
+    // last row (visibility is monotone in t).  Skipping at this level, not
+    // inside the tile body, keeps the tile code's register allocation: an
+    // early return there cost the causal kernels 54 registers.  With one
+    // workgroup per CU every wave computes every tile (fully masked tiles
+    // give p = 0): the workgroup waits for its last wave either way.
+    if (OCC >= 2 && q0w >= p.Sq) {
+      idle_tiles(n_tiles);
     } else {
       run(n_full, std::integral_constant<bool, false>{});
-      run(n_tiles, std::integral_constant<bool, true>{});
+      const int n_act = (CAUSAL && OCC >= 2) ? max(n_full, min(n_tiles, wave_last_q / BN + 1)) : n_tiles;
+      run(n_act, std::integral_constant<bool, true>{});
+      idle_tiles(n_tiles);
     }
 #ifdef FA_TIMING
     tm_epi0 = FA_CLK() - tm0;
