@@ -169,6 +169,7 @@ def _fmt(v, precision=3):
 def run_passes(out: Path, target: list[str], plan=None, timeout=120) -> dict:
     """Run one rocprofv3 process per pass of `plan` over the command `target`."""
     plan = METRIC_PLAN if plan is None else plan
+    cwd = Path.cwd()
     out = Path(out).resolve()
     out.mkdir(parents=True, exist_ok=True)
     # The passes run from /tmp: make the command's relative file arguments
@@ -191,6 +192,8 @@ def run_passes(out: Path, target: list[str], plan=None, timeout=120) -> dict:
         if proc.returncode != 0:
             raise RuntimeError(f"rocprofv3 pass {name} failed ({proc.returncode}); see {out / (name + '.log')}")
         summary[name] = summarize_pass(pdir)
+        # Recorded relative to the caller's directory (the passes ran from /tmp).
+        summary[name]["profiler_output"] = os.path.relpath(pdir, cwd)
     return summary
 
 
