@@ -205,19 +205,26 @@ __device__ __forceinline__ int vt_pos(int k) {
 // at the top of a tile so its latency hides behind the tile.  Each of those
 // workgroups takes exactly one ticket past the end and stops, so the taker of
 // raw count n_tiles - 1 is the last user of the counter and resets it to 0:
-// the next launch (or a replay of this one) finds it clean.  The counters
-// live in a device array owned by the library, one group of kQueues per
-// launch slot (one 128-byte line per counter); launch slots rotate over
-// kQueueSlots, which bounds the launches that may be in flight on one device.
+// the next launch finds it clean.  The counters live in a device array owned
+// by the library, one group of kQueues per launch slot (one 128-byte line per
+// counter); launch slots rotate over kQueueSlots, which bounds the eager
+// launches that may be in flight on one device.
+//
+// A launch recorded into a graph (its stream is capturing) gets no counters
+// (KernelArgs::queue == nullptr): its workgroups walk the same heaviest-first
+// ticket order statically, workgroup w of a queue taking tickets w, w + W,
+// w + 2W, ...  Replays of captured launches therefore share no device state
+// with each other or with eager launches, whatever streams they run on.
 constexpr int kQueues = 8;
 constexpr int kQueueSlots = 1024;
 constexpr int kQueueStride = 16;  // 128 bytes between counters
 __device__ unsigned long long g_tile_queues[kQueueSlots * kQueues * kQueueStride];
 
 struct TileQueue {
-  unsigned long long *ctr;
+  unsigned long long *ctr;  // null: static schedule (graph-captured launch)
   uint32_t n_tiles;   // tiles of this queue
   uint32_t n_static;  // tickets taken without the counter: min(workers, n_tiles)
+  uint32_t workers;   // workgroups serving this queue
   int x, nq, nh;      // queue index, queue count, heads of this queue
 
   __device__ __forceinline__ TileQueue(const KernelArgs &p) {
@@ -226,13 +233,18 @@ struct TileQueue {
     const int BH = p.B * p.H;
     nh = (BH - x + nq - 1) / nq;
     n_tiles = (uint32_t)nh * (uint32_t)p.n_mtiles * (uint32_t)p.kv_splits;
-    const uint32_t workers = (gridDim.x - x + nq - 1) / nq;
+    workers = (gridDim.x - x + nq - 1) / nq;
     n_static = workers < n_tiles ? workers : n_tiles;
-    ctr = p.queue + x * kQueueStride;
+    ctr = p.queue != nullptr ? p.queue + x * kQueueStride : nullptr;
   }
   __device__ __forceinline__ uint32_t first() const { return blockIdx.x / nq; }
-  __device__ __forceinline__ unsigned long long request() const { return atomicAdd(ctr, 1ull); }
-  __device__ __forceinline__ uint32_t finish(unsigned long long raw) const {
+  __device__ __forceinline__ unsigned long long request() const {
+    return ctr != nullptr ? atomicAdd(ctr, 1ull) : 0ull;
+  }
+  // Ticket of this workgroup's unit it + 1, given the counter value that
+  // request() returned during unit it.
+  __device__ __forceinline__ uint32_t finish(unsigned long long raw, int it) const {
+    if (ctr == nullptr) return first() + (uint32_t)(it + 1) * workers;
     if (raw == n_tiles - 1) atomicExch(ctr, 0ull);
     return n_static + (uint32_t)raw;
   }
@@ -965,7 +977,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
     // The empty DMAs issued during the last KV tile write zeros into a
     // stage: let them land before the next tile's DMAs target it.
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    if (threadIdx.x == 0) s_ticket[(it + 1) & 1] = tq.finish(next_raw);
+    if (threadIdx.x == 0) s_ticket[(it + 1) & 1] = tq.finish(next_raw, it);
     __syncthreads();  // LDS reuse by the next tile, ticket broadcast
   }
 }
@@ -1389,7 +1401,7 @@ fa_fwd_pp_kernel(KernelArgs p) {
     // The DMAs issued past the last tile may still be writing zeros into the
     // rings: retire them (every wave) before a next tile reuses the slots.
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    if (threadIdx.x == 0) s_ticket[(it + 1) & 1] = tq.finish(next_raw);
+    if (threadIdx.x == 0) s_ticket[(it + 1) & 1] = tq.finish(next_raw, it);
     __syncthreads();
   }
 }
@@ -1692,11 +1704,21 @@ int launch(const fa_fwd_params *p, void *hip_stream, int splits, void *workspace
   a.split_tiles = splits > 1 ? plan.split_tiles : (1 << 30);
   a.part_o = splits > 1 ? (float *)workspace : nullptr;
   a.part_lse = splits > 1 ? (float *)((char *)workspace + split_part_o_bytes(p, splits)) : nullptr;
+  hipStream_t stream = (hipStream_t)hip_stream;
   {
-    unsigned long long *base = queue_base(device);
-    if (base == nullptr) return FA_ERR_LAUNCH;
-    const unsigned long long seq = g_launch_seq.fetch_add(1, std::memory_order_relaxed);
-    a.queue = base + (seq % kQueueSlots) * kQueues * kQueueStride;
+    // A launch recorded into a graph takes no counters (static schedule, see
+    // TileQueue); an eager one takes the next launch slot.  A failed query
+    // is treated as capture: the static schedule is always safe.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone;
+    if (capturing) {
+      a.queue = nullptr;
+    } else {
+      unsigned long long *base = queue_base(device);
+      if (base == nullptr) return FA_ERR_LAUNCH;
+      const unsigned long long seq = g_launch_seq.fetch_add(1, std::memory_order_relaxed);
+      a.queue = base + (seq % kQueueSlots) * kQueues * kQueueStride;
+    }
     const int64_t bh = (int64_t)p->B * p->H;
     int64_t nq = kQueues;
     if (nq > plan.grid) nq = plan.grid;
@@ -1722,7 +1744,6 @@ int launch(const fa_fwd_params *p, void *hip_stream, int splits, void *workspace
   a.c = c;
   a.timing = g_timing_buffer;
 
-  hipStream_t stream = (hipStream_t)hip_stream;
   hipLaunchKernelGGL(e.fn, dim3(plan.grid), dim3(64 * e.NW), 0, stream, a);
   if (hipGetLastError() != hipSuccess) return FA_ERR_LAUNCH;
   if (splits > 1) {

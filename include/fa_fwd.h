@@ -11,8 +11,18 @@
  *
  * Conventions
  *  - Every tensor pointer is a DEVICE pointer owned by the caller.  The
- *    library allocates nothing, keeps no mutable global state and launches on
- *    the stream it is given; it is reentrant.
+ *    library allocates nothing and launches on the stream it is given.
+ *  - Device state: the persistent grid pulls its tiles from queue counters
+ *    in a library-owned __device__ array (per device: 1024 launch slots of
+ *    8 counters).  An eager launch takes the next slot and leaves its
+ *    counters at zero when it completes, so at most 1023 eager launches may
+ *    be queued or running on one device at a time, over all streams and
+ *    threads; more would share counters and race.  A launch made while its
+ *    stream is capturing (graph) uses no counters (a static tile schedule),
+ *    so graph replays share no device state with each other or with eager
+ *    launches.
+ *  - Host state: a launch sequence number and per-device caches (CU count,
+ *    counter address), all atomic: calls may come from any thread.
  *  - Strides are in ELEMENTS, in (batch, head, seq, dim) order.  The dim
  *    stride must be 1; the other strides must be non-negative multiples of 8
  *    elements, the seq stride at least D when the sequence has more than one

@@ -1,12 +1,13 @@
 """GPU: the persistent grid's tile queues.
 
-Every launch pulls its tiles from device-side queue counters that the last
-user of each queue resets to zero, in one of 1024 launch slots.  These tests
-check the contract that makes that safe: results never depend on the slot, on
-what earlier launches left behind, on replays of a captured graph, or on two
-streams interleaving launches.  Each result is compared bit for bit with an
-eager reference launch (same kernel, same inputs: the tile order never changes
-a tile's arithmetic).
+Every eager launch pulls its tiles from device-side queue counters that the
+last user of each queue resets to zero, in one of 1024 launch slots; a launch
+recorded into a graph walks the same tile order statically, with no counters.
+These tests check the contract that makes that safe: results never depend on
+the slot, on what earlier launches left behind, on replays of captured graphs
+(also concurrent ones), or on streams interleaving launches.  Each result is
+compared bit for bit with an eager reference launch (same kernel, same inputs:
+the tile order never changes a tile's arithmetic).
 """
 
 from __future__ import annotations
@@ -65,6 +66,46 @@ def test_graph_replays(fa):
         again = fa.attention(q, k, v, True, 0.1)
         torch.cuda.synchronize()
         assert torch.equal(again, want_o)
+
+
+def test_concurrent_graph_replays(fa):
+    """Captured launches use a static tile schedule (no queue counters): two graphs
+    replayed concurrently on two streams, with eager launches on a third stream taking
+    launch slots meanwhile, all match an eager reference bit for bit."""
+    q, k, v = _inputs(26, (2, 8, 900, 128))
+    want_o, want_l = fa.attention(q, k, v, True, 0.1, return_lse=True)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fa.attention(q, k, v, True, 0.1, return_lse=True)  # warm-up on a side stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graphs, outs = [], []
+    for _ in range(2):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs.append(fa.attention(q, k, v, True, 0.1, return_lse=True))
+        graphs.append(g)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream(), torch.cuda.Stream()]
+    eager = []
+    for rep in range(6):
+        for o, l in outs:
+            o.zero_()
+            l.zero_()
+        torch.cuda.synchronize()
+        for g, st in zip(graphs, streams[:2]):
+            with torch.cuda.stream(st):
+                g.replay()
+        with torch.cuda.stream(streams[2]):
+            for _ in range(3):
+                eager.append(fa.attention(q, k, v, True, 0.1))
+        torch.cuda.synchronize()
+        for o, l in outs:
+            assert torch.equal(o, want_o) and torch.equal(l, want_l), rep
+    for o in eager:
+        assert torch.equal(o, want_o)
 
 
 def test_two_streams(fa):
