@@ -1650,6 +1650,34 @@ bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 }  // namespace
 
+// Split-KV partial results of fa_fwd_split_static: a library-owned buffer of
+// FA_STATIC_SCRATCH_BYTES per device (held until the process ends), for
+// callers that cannot allocate.  Every call on a device shares it; each call
+// writes every partial it later reads (all KV runs of every row < Sq), so
+// nothing needs clearing between calls.  In host code `scratch` names a
+// host-side stand-in: the device address comes from hipGetSymbolAddress.
+static __device__ __align__(256) char scratch[FA_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+// Device address of `scratch`, asked once per device with that device
+// current (each device holds its own copy of the array).
+std::atomic<char *> g_scratch_base[kMaxDevices];
+
+char *static_scratch_base(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  char *ptr = g_scratch_base[device].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    void *addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || addr == nullptr) return nullptr;
+    ptr = (char *)addr;
+    g_scratch_base[device].store(ptr, std::memory_order_release);
+  }
+  return ptr;
+}
+
+}  // namespace
+
 #ifdef FA_TIMING
 static uint32_t *g_timing_buffer = nullptr;
 extern "C" void fa_set_timing_buffer(void *p) { g_timing_buffer = (uint32_t *)p; }
@@ -1784,6 +1812,7 @@ const char *fa_error_string(int code) {
     case FA_ERR_TILING: return "unsupported BLOCK_M/BLOCK_N combination";
     case FA_ERR_SCALE: return "sm_scale must be finite";
     case FA_ERR_GRID: return "the persistent program count must be >= 0";
+    case FA_ERR_SCRATCH: return "the split-KV partial results exceed the library's static scratch buffer (FA_STATIC_SCRATCH_BYTES)";
     case FA_ERR_LAUNCH: return "the HIP runtime rejected the kernel launch";
     default: return "unknown fa_fwd status";
   }
@@ -1876,6 +1905,19 @@ int fa_fwd_split(const fa_fwd_params *p, int32_t kv_splits, void *workspace, int
                  void *hip_stream) {
   if (kv_splits < 1 || kv_splits > kMaxKvSplits) return FA_ERR_GRID;
   return launch(p, hip_stream, kv_splits, workspace, workspace_bytes);
+}
+
+int fa_fwd_split_static(const fa_fwd_params *p, int32_t kv_splits, void *hip_stream) {
+  if (kv_splits < 1 || kv_splits > kMaxKvSplits) return FA_ERR_GRID;
+  const int rc = fa_validate(p);
+  if (rc != FA_OK) return rc;
+  if (kv_splits == 1) return launch(p, hip_stream, 1, nullptr, 0);
+  if (split_workspace_bytes(p, kv_splits) > (int64_t)FA_STATIC_SCRATCH_BYTES) return FA_ERR_SCRATCH;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return FA_ERR_LAUNCH;
+  char *base = static_scratch_base(device);
+  if (base == nullptr) return FA_ERR_LAUNCH;
+  return launch(p, hip_stream, kv_splits, base, (int64_t)FA_STATIC_SCRATCH_BYTES);
 }
 
 int32_t fa_default_kv_splits(const fa_fwd_params *p) {

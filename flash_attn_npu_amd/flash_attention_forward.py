@@ -67,7 +67,7 @@ DEFAULT_TILING_PRESETS = {
 
 FA_OK = 0
 FA_ERR_LAUNCH = -100
-_ARGUMENT_ERRORS = {-1, -2, -3, -4, -5, -6, -7, -8, -9}
+_ARGUMENT_ERRORS = {-1, -2, -3, -4, -5, -6, -7, -8, -9, -10}
 FA_CFG_COUNT = 8
 FA_DTYPE = {torch.float16: 0, torch.bfloat16: 1}
 # fp8-e5m2 V with fp16 / bf16 q, k, o: dtype code + FA_DTYPE_V_E5M2_OFFSET
@@ -155,6 +155,8 @@ def _load_library():
     lib.fa_split_workspace_bytes.restype = ctypes.c_int64
     lib.fa_fwd_split.argtypes = [P, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
     lib.fa_fwd_split.restype = ctypes.c_int
+    lib.fa_fwd_split_static.argtypes = [P, ctypes.c_int32, ctypes.c_void_p]
+    lib.fa_fwd_split_static.restype = ctypes.c_int
     lib.fa_default_kv_splits.argtypes = [P]
     lib.fa_default_kv_splits.restype = ctypes.c_int32
     if lib.fa_params_size() != ctypes.sizeof(FaFwdParams):

@@ -21,8 +21,11 @@
  *    stream is capturing (graph) uses no counters (a static tile schedule),
  *    so graph replays share no device state with each other or with eager
  *    launches.
+ *    fa_fwd_split_static also keeps its split-KV partial results in a
+ *    library-owned __device__ buffer (see there).
  *  - Host state: a launch sequence number and per-device caches (CU count,
- *    counter address), all atomic: calls may come from any thread.
+ *    counter and scratch addresses), all atomic: calls may come from any
+ *    thread.
  *  - Strides are in ELEMENTS, in (batch, head, seq, dim) order.  The dim
  *    stride must be 1; the other strides must be non-negative multiples of 8
  *    elements, the seq stride at least D when the sequence has more than one
@@ -72,6 +75,7 @@ enum fa_status {
   FA_ERR_TILING = -7,      /* block_m/block_n/num_waves: unsupported combination  */
   FA_ERR_SCALE = -8,       /* sm_scale is NaN or infinite                         */
   FA_ERR_GRID = -9,        /* persistent grid size is negative                    */
+  FA_ERR_SCRATCH = -10,    /* split workspace larger than FA_STATIC_SCRATCH_BYTES */
   FA_ERR_LAUNCH = -100,    /* the HIP runtime rejected the launch                 */
 };
 
@@ -166,6 +170,18 @@ int fa_fwd_split(const fa_fwd_params *p, int32_t kv_splits, void *workspace, int
  * unsplit grid would fill less than half of the resident workgroup slots and
  * each run keeps at least 8 KV tiles.  Host-only. */
 int32_t fa_default_kv_splits(const fa_fwd_params *p);
+
+/* ---- No-allocation split-KV.  No counterpart in the reference.  For callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc): fa_fwd_split with the
+ * partial results in a library-owned static device buffer of
+ * FA_STATIC_SCRATCH_BYTES per device (held until the process ends) instead of
+ * a caller workspace; it calls no allocator.  FA_ERR_SCRATCH when
+ * fa_split_workspace_bytes(p, kv_splits) exceeds the buffer.  Calls that
+ * overlap on one device (any streams, including graph replays) share the
+ * buffer and race: serialise them.  kv_splits == 1 is fa_fwd. */
+#define FA_STATIC_SCRATCH_BYTES (32 * 1024 * 1024)
+int fa_fwd_split_static(const fa_fwd_params *p, int32_t kv_splits, void *hip_stream);
 
 #ifdef __cplusplus
 }

@@ -358,3 +358,13 @@ def test_split_argument_errors_before_launch(lib):
     assert lib.fa_fwd_split(ctypes.byref(p), 4, None, 1 << 20, None) == -1
     assert lib.fa_fwd_split(ctypes.byref(p), 4, (1 << 40), 16, None) == -2
     assert lib.fa_fwd_split(ctypes.byref(p), 4, (1 << 40) + 64, 1 << 30, None) == -6
+
+
+def test_static_split_argument_errors_before_launch(lib):
+    """fa_fwd_split_static checks its split count and the scratch limit before any HIP call."""
+    p = _params(shape=(2, 16, 4096, 128))
+    assert lib.fa_fwd_split_static(ctypes.byref(p), 0, None) == -9
+    assert lib.fa_fwd_split_static(ctypes.byref(p), 65, None) == -9
+    assert lib.fa_split_workspace_bytes(ctypes.byref(p), 3) > 32 * 1024 * 1024
+    assert lib.fa_fwd_split_static(ctypes.byref(p), 3, None) == -10
+    assert b"static scratch" in lib.fa_error_string(-10)
