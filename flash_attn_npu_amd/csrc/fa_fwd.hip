@@ -677,7 +677,10 @@ fa_fwd_dma_kernel(KernelArgs p) {
       // VPF V^T fragments of the P*V product are issued right behind the K
       // reads so they land during the softmax.
       constexpr int NQK = (D / 16) * (BN / 32);
-      constexpr int KPF = 4;
+      // K fragments read KPF MFMAs ahead (3 in the three-workgroups-per-CU
+      // D = 128 kernel, whose 168 registers hold no fourth fragment without
+      // spilling).
+      constexpr int KPF = (OCC >= 3 && D == 128) ? 3 : 4;
       constexpr int NPV = V8 ? (BN / 64) * C::DB : (BN / 16) * C::DB;
       constexpr int VPF = V8 ? 1 : 2;
       constexpr int VRD = V8 ? 4 : 2;  // LDS reads per V^T fragment
@@ -917,6 +920,13 @@ fa_fwd_dma_kernel(KernelArgs p) {
     tm_epi0 = FA_CLK() - tm0;
 #endif
 
+    // The DMAs issued during the last KV tile (zeros into the free stage)
+    // must land before the next unit's DMAs target that stage.  Wait for
+    // them here, before the output stores: vmcnt retires in issue order, so
+    // a wait after the stores would also wait for their write acknowledgement
+    // (a memory round trip per unit), which the next unit's first wait now
+    // overlaps with its own loads.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     const float l_tot = MSUM ? lacc[0] : halves_sum(l_run);
     if (p.kv_splits > 1) {
       // Partial result of this KV run: O normalised by its own row sum, in
@@ -974,9 +984,6 @@ fa_fwd_dma_kernel(KernelArgs p) {
       dst[13] = tm_dma; dst[14] = tm_idle;
     }
 #endif
-    // The empty DMAs issued during the last KV tile write zeros into a
-    // stage: let them land before the next tile's DMAs target it.
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     if (threadIdx.x == 0) s_ticket[(it + 1) & 1] = tq.finish(next_raw, it);
     __syncthreads();  // LDS reuse by the next tile, ticket broadcast
   }
@@ -1513,8 +1520,10 @@ const KernelEntry kKernels[] = {
     FA_DMA_ENTRIES(64, 32, 4, 2, 2),
     FA_DMA_ENTRIES(64, 128, 4, 2, 2),
     // D = 256: 512 registers per wave (O^T alone is 128), so one workgroup
-    // per CU; 32-key tiles keep S, P and the operand fragments small.
+    // per CU; 32-key tiles keep S, P and the operand fragments small.  The
+    // 64-key kernels are candidates for the tile sweep.
     FA_DMA_ENTRIES(256, 32, 4, 2, 1),
+    FA_DMA_ENTRIES(256, 64, 4, 2, 1),
     // D = 32: four workgroups per CU when causal (8-9% faster than two);
     // non-causal measured 1.7% slower at four, so it keeps two.
     entry_dma<32, 64, 4, 2, 2, false, false>(), entry_dma<32, 64, 4, 2, 4, false, true>(),

@@ -268,15 +268,27 @@ def _resolve_tiling(z, h, n_ctx, head_dim, causal, bm=None, bn=None):
     return (*get_tiling(z, h, n_ctx, head_dim, causal), get_tiling_source(z, h, n_ctx, head_dim, causal))
 
 
-def _describe_runtime(z, h, n_ctx, head_dim, causal, bm=None, bn=None):
+def _describe_runtime(z, h, n_ctx, head_dim, causal, bm=None, bn=None, dtype=torch.float16, v_dtype=None):
+    """What a call with this shape would launch (flash_attention_forward.py:634-644).
+
+    dtype is the q/k/o element type and v_dtype V's (None: the same; float8_e5m2 selects
+    the fp8-V kernels, as _launch_kernel does).
+    """
     block_m, block_n, tiling_source = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn)
-    cfg = _query_config(z, h, n_ctx, head_dim, causal, block_m, block_n,
-                        programs=_get_persistent_programs())
+    fp8_v = v_dtype == FP8_V_DTYPE
+    if fp8_v and tiling_source != "override":
+        block_m, block_n = fp8_v_tiling(head_dim)
+    programs = _get_persistent_programs()
+    lib = _load_library()
+    p = _shape_params(z, h, n_ctx, head_dim, causal, block_m, block_n, dtype, programs)
+    if fp8_v:
+        p.dtype += FA_DTYPE_V_E5M2_OFFSET
+    out = (ctypes.c_int32 * FA_CFG_COUNT)()
+    _check(lib.fa_query_config(ctypes.byref(p), out), "fa_query_config")
+    cfg = list(out)
     splits = _get_kv_splits()
     if splits == 0:
-        p = _shape_params(z, h, n_ctx, head_dim, causal, block_m, block_n, torch.float16,
-                          _get_persistent_programs())
-        splits = int(_load_library().fa_default_kv_splits(ctypes.byref(p)))
+        splits = int(lib.fa_default_kv_splits(ctypes.byref(p)))
     return {
         "selected_config": {"BLOCK_M": cfg[0], "BLOCK_N": cfg[1]},
         "tiling_source": tiling_source,
@@ -315,16 +327,64 @@ def _validate_inputs(q, k, v):
 
 
 def _kernel_ready(t):
-    """A view the kernel can read directly: dim stride 1, 16-byte rows, 16B-aligned."""
-    if t.is_contiguous() and t.data_ptr() % 16 == 0:
+    """A view the kernel can read directly: dim stride 1, 16-byte rows, 16B-aligned base.
+
+    Anything else is copied into a fresh dense tensor (whose base the caching allocator
+    aligns), including a contiguous view at an odd storage offset: contiguous() would
+    return that same misaligned view.
+    """
+    ptr = t.data_ptr()
+    if ptr % 16 == 0 and t.is_contiguous():
         return t  # rows of D >= 16 elements: every stride is a multiple of 16 bytes
     st = t.stride()
     align = 16 // t.element_size()
-    if st[3] != 1 or any(s % align for s in st[:3]) or t.data_ptr() % 16:
-        return t.contiguous()
-    if t.shape[2] > 1 and st[2] < t.shape[3]:
-        return t.contiguous()
+    if ptr % 16 or st[3] != 1 or any(s % align for s in st[:3]) or (t.shape[2] > 1 and st[2] < t.shape[3]):
+        return t.clone(memory_format=torch.contiguous_format)
     return t
+
+
+class _LaunchPlan:
+    """Everything a launch needs that depends only on the call's configuration:
+    the parameter block (shape, strides, dtype, mask, tiling, program count), the
+    split count and its workspace size.  Built once per configuration."""
+
+    __slots__ = ("params", "splits", "workspace_bytes")
+
+    def __init__(self, params, splits, workspace_bytes):
+        self.params = params
+        self.splits = splits
+        self.workspace_bytes = workspace_bytes
+
+
+# Launch plans keyed by (shapes, strides, dtypes, causal, resolved tiling, program
+# count, split override): a call only copies the block and sets its pointers and scale.
+_PLANS = {}
+
+
+def _launch_plan(lib, q, k, v, out, causal, bm, bn, programs, split_env):
+    key = (q.shape, q.stride(), k.stride(), v.stride(), out.stride(), q.dtype, v.dtype, causal, bm, bn,
+           programs, split_env)
+    plan = _PLANS.get(key)
+    if plan is not None:
+        return plan
+    z, h, n_ctx, head_dim = q.shape
+    p = FaFwdParams()
+    p.q_stride[:] = q.stride()
+    p.k_stride[:] = k.stride()
+    p.v_stride[:] = v.stride()
+    p.o_stride[:] = out.stride()
+    p.B, p.H, p.Sq, p.Sk, p.D = z, h, n_ctx, n_ctx, head_dim
+    p.dtype = FA_DTYPE[q.dtype] + (FA_DTYPE_V_E5M2_OFFSET if v.dtype == FP8_V_DTYPE else 0)
+    p.causal = 1 if causal else 0
+    p.block_m, p.block_n = int(bm), int(bn)
+    p.num_programs = programs
+    splits = split_env if split_env else int(lib.fa_default_kv_splits(ctypes.byref(p)))
+    nbytes = 0
+    if splits > 1:
+        nbytes = int(lib.fa_split_workspace_bytes(ctypes.byref(p), splits))
+        _check(nbytes if nbytes < 0 else 0, "fa_split_workspace_bytes")
+    plan = _PLANS[key] = _LaunchPlan(p, splits, nbytes)
+    return plan
 
 
 def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
@@ -334,9 +394,9 @@ def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
     """
     _validate_inputs(q, k, v)
     z, h, n_ctx, head_dim = q.shape
-    fp8_v = v.dtype == FP8_V_DTYPE
+    causal = bool(causal)
     bm, bn, source = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn)
-    if fp8_v and source != "override":
+    if v.dtype == FP8_V_DTYPE and source != "override":
         bm, bn = fp8_v_tiling(head_dim)  # the fp8-V kernels' one tiling; presets are for 16-bit V
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     out = torch.empty_like(q)
@@ -349,39 +409,27 @@ def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
         raise ValueError("sm_scale must be finite")
 
     lib = _load_library()
-    p = FaFwdParams()
+    plan = _launch_plan(lib, q, k, v, out, causal, bm, bn, _get_persistent_programs(), _get_kv_splits())
+    p = FaFwdParams.from_buffer_copy(plan.params)
     p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
-    p.q_stride[:] = q.stride()
-    p.k_stride[:] = k.stride()
-    p.v_stride[:] = v.stride()
-    p.o_stride[:] = out.stride()
-    p.B, p.H, p.Sq, p.Sk, p.D = z, h, n_ctx, n_ctx, head_dim
-    p.dtype = FA_DTYPE[q.dtype] + (FA_DTYPE_V_E5M2_OFFSET if fp8_v else 0)
-    p.causal = 1 if causal else 0
     p.sm_scale = sm_scale
-    p.block_m, p.block_n = int(bm), int(bn)
-    p.num_programs = _get_persistent_programs()
-    pp = ctypes.byref(p)
-    splits = _get_kv_splits()
-    if splits == 0:
-        splits = int(lib.fa_default_kv_splits(pp))
     dev = q.device.index
     if dev == torch.cuda.current_device():
-        _launch_on(lib, pp, splits, dev, q.device)
+        _launch_on(lib, p, plan, dev, q.device)
     else:
         with torch.cuda.device(dev):
-            _launch_on(lib, pp, splits, dev, q.device)
+            _launch_on(lib, p, plan, dev, q.device)
     return out, lse
 
 
-def _launch_on(lib, pp, splits, dev, device):
+def _launch_on(lib, p, plan, dev, device):
     """Launch on the current stream of device `dev` (the current device)."""
     stream = _current_raw_stream(dev)
-    if splits > 1:
-        nbytes = int(lib.fa_split_workspace_bytes(pp, splits))
-        _check(nbytes if nbytes < 0 else 0, "fa_split_workspace_bytes")
-        workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)  # caching allocator: 512 B aligned
-        _check(lib.fa_fwd_split(pp, splits, workspace.data_ptr(), nbytes, stream), "fa_fwd_split")
+    pp = ctypes.byref(p)
+    if plan.splits > 1:
+        workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)  # 512 B aligned
+        _check(lib.fa_fwd_split(pp, plan.splits, workspace.data_ptr(), plan.workspace_bytes, stream),
+               "fa_fwd_split")
     else:
         _check(lib.fa_fwd(pp, stream), "fa_fwd")
 

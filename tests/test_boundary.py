@@ -266,6 +266,13 @@ def test_kernel_ready_fast_path_and_copies():
     odd = torch.zeros((1, 2, 40, 72), dtype=torch.float16)[..., 1:65]  # misaligned base
     ready = fa._kernel_ready(odd)
     assert ready is not odd and ready.is_contiguous() and torch.equal(ready, odd)
+    # A contiguous view at an odd storage offset: contiguous() would hand back the
+    # same misaligned view, so the module must copy it.
+    buf = torch.arange(2 * 3 * 40 * 64 + 1, dtype=torch.float32).to(torch.float16)
+    shifted = buf[1:].view(2, 3, 40, 64)
+    assert shifted.is_contiguous() and shifted.data_ptr() % 16 == 2
+    ready = fa._kernel_ready(shifted)
+    assert ready is not shifted and ready.data_ptr() % 16 == 0 and torch.equal(ready, shifted)
 
 
 def test_persistent_programs_env(monkeypatch):
@@ -284,6 +291,20 @@ def test_describe_runtime_keys(monkeypatch):
     assert set(rt) >= {"selected_config", "tiling_source", "total_tiles", "launched_programs", "stage"}
     assert rt["stage"] == 3 and rt["launched_programs"] == min(rt["total_tiles"], 8 // rt["waves"] * 256)
     assert fa._describe_runtime(4, 32, 2048, 128, False)["stage"] == 1
+
+
+def test_describe_runtime_follows_dtype(monkeypatch):
+    """The description queries the kernel the call would launch: an fp8-e5m2 V selects the
+    fp8-V kernels' tiling (64-key tiles), a bf16 call the bf16 kernel."""
+    monkeypatch.delenv("PERSISTENT_PROGRAMS", raising=False)
+    monkeypatch.delenv("KV_SPLITS", raising=False)
+    plain = fa._describe_runtime(1, 2, 300, 128, False, dtype=torch.bfloat16)
+    fp8 = fa._describe_runtime(1, 2, 300, 128, False, dtype=torch.bfloat16, v_dtype=torch.float8_e5m2)
+    assert fp8["selected_config"] == {"BLOCK_M": 128, "BLOCK_N": 64}
+    assert fp8["kernel_id"] != plain["kernel_id"]
+    rows = fa.kernel_table()
+    assert rows[plain["kernel_id"]]["dtype"] == "bfloat16"
+    assert rows[fp8["kernel_id"]]["dtype"] == "bfloat16+float8_e5m2_v"
 
 
 def test_check_maps_errors():
