@@ -148,7 +148,7 @@ def main(argv=None):
     log(f"workload: {w.describe()} sm_scale={w.sm_scale:.6f}")
     q, k, v = make_inputs(w, device="cuda")
     torch.cuda.synchronize()
-    rt = fa._describe_runtime(w.B, w.H, w.S, w.D, w.causal)
+    rt = fa._describe_runtime(w.B, w.H, w.S, w.D, w.causal, dtype=w.dtype)
     log(f"runtime: {rt}")
 
     def step():

@@ -10,6 +10,7 @@ travels with the source tree.
 
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -19,6 +20,7 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 REPO_DIR = PKG_DIR.parent
 SRC = PKG_DIR / "csrc" / "fa_fwd.hip"
+PLAN_SRC = PKG_DIR / "csrc" / "fa_plan.cpp"  # included by fa_fwd.hip
 INCLUDE_DIR = REPO_DIR / "include"
 LIB_NAME = "libfa_mi355x.so"
 LIB_PATH = PKG_DIR / LIB_NAME
@@ -30,6 +32,21 @@ def hipcc_path() -> str:
         if cand and Path(cand).exists():
             return cand
     raise RuntimeError("hipcc not found: install ROCm or set HIPCC")
+
+
+def source_hash() -> str:
+    """sha256 (first 16 hex digits) of the kernel source, the host planning
+    source it includes and the ABI header.
+
+    Compiled into the library as fa_build_id(), so a library older than its
+    sources is detectable without a GPU.
+    """
+    h = hashlib.sha256()
+    for path in (SRC, PLAN_SRC, INCLUDE_DIR / "fa_fwd.h"):
+        h.update(path.name.encode())
+        h.update(b"\0")
+        h.update(path.read_bytes())
+    return h.hexdigest()[:16]
 
 
 def compile_command(out: Path = LIB_PATH, extra: list[str] | None = None) -> list[str]:
@@ -44,6 +61,7 @@ def compile_command(out: Path = LIB_PATH, extra: list[str] | None = None) -> lis
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument",
         f"-I{INCLUDE_DIR}",
+        f'-DFA_SOURCE_HASH="{source_hash()}"',
         *(extra or []),
         "-o", str(out),
         str(SRC),

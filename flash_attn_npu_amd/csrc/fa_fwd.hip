@@ -50,8 +50,12 @@
 
 #include <atomic>
 #include <type_traits>
+#include <utility>
 
 #include "fa_fwd.h"
+// Host-only planning and the kernel table's metadata (plain C++, also built on
+// its own for the host sanitizer test).
+#include "fa_plan.cpp"
 
 namespace {
 
@@ -70,8 +74,6 @@ constexpr float kLn2 = 0.6931471805599453f;
 // The running max only moves when a row max exceeds it by more than this many
 // log2 units, so un-normalised probabilities stay <= 2^8 (safe in fp16/bf16).
 constexpr float kLazyMaxThreshold = 8.0f;
-constexpr int kMaxBlockM = 256;  // largest BLOCK_M of any kernel instance
-constexpr int kRowMargin = 1024; // rows addressed past a tensor's end (>= BLOCK_M, >= NR * BLOCK_N)
 // FA_TIMING (development builds only): the ping-pong kernel accumulates, per
 // wave, the shader-clock cycles spent in each phase and writes them to
 // KernelArgs::timing.  The product build compiles none of it.
@@ -1468,159 +1470,32 @@ __global__ void __launch_bounds__(256) fa_merge_kernel(MergeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Kernel table.
+// Kernel table: kKernelFns[i] is the kernel that kKernelMeta[i] (fa_plan.cpp)
+// describes, instantiated from that entry's parameters; the LDS bytes the
+// planner reports are checked against each kernel's own layout.
 typedef void (*KernelFn)(KernelArgs);
 
-struct KernelEntry {
-  int32_t D, dtype, causal, BN, NW;
-  int32_t stages;     // LDS stages in the K/V ring
-  int32_t lds_bytes;
-  int32_t wg_per_cu;  // resident workgroups per CU (registers and LDS)
-  bool splittable;    // supports split-KV (partial outputs + merge)
-  KernelFn fn;
-};
-
-template <int D, int BN, int NW, int NSTAGE, int OCC, bool BF16, bool CAUSAL, bool V8 = false>
-constexpr KernelEntry entry_dma() {
-  return KernelEntry{D, (BF16 ? FA_DTYPE_BF16 : FA_DTYPE_FP16) + (V8 ? 2 : 0), CAUSAL ? 1 : 0, BN, NW, NSTAGE,
-                     Cfg2<D, BN, NW, NSTAGE, OCC, V8>::LDS_BYTES, OCC, true,
-                     fa_fwd_dma_kernel<D, BN, NW, NSTAGE, OCC, BF16, CAUSAL, V8>};
-}
-
-#define FA_PP_ENTRIES(D, BN, NR)                                                                     \
-  KernelEntry{D, 0, 0, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, false, fa_fwd_pp_kernel<D, BN, NR, false, false>}, \
-  KernelEntry{D, 0, 1, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, false, fa_fwd_pp_kernel<D, BN, NR, false, true>},  \
-  KernelEntry{D, 1, 0, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, false, fa_fwd_pp_kernel<D, BN, NR, true, false>},  \
-  KernelEntry{D, 1, 1, BN, 8, NR, Cfg3<D, BN, NR>::LDS_BYTES, 1, false, fa_fwd_pp_kernel<D, BN, NR, true, true>}
-#define FA_DMA_ENTRIES(D, BN, NW, ST, OCC)                                                     \
-  entry_dma<D, BN, NW, ST, OCC, false, false>(), entry_dma<D, BN, NW, ST, OCC, false, true>(), \
-      entry_dma<D, BN, NW, ST, OCC, true, false>(), entry_dma<D, BN, NW, ST, OCC, true, true>()
-
-// fp8-e5m2 V with fp16 / bf16 Q, K, O (dtype codes FA_DTYPE_*_V_E5M2).
-#define FA_DMA8_ENTRIES(D, BN, NW, ST, OCC)                                                                  \
-  entry_dma<D, BN, NW, ST, OCC, false, false, true>(), entry_dma<D, BN, NW, ST, OCC, false, true, true>(), \
-      entry_dma<D, BN, NW, ST, OCC, true, false, true>(), entry_dma<D, BN, NW, ST, OCC, true, true, true>()
-
-// The first entry matching (D, dtype, causal, BLOCK_N, waves) serves a launch.
-const KernelEntry kKernels[] = {
-    FA_DMA_ENTRIES(128, 64, 4, 2, 2),
-    FA_PP_ENTRIES(128, 64, 4),
-    // D = 128, 32-key tiles: the non-causal default, at three workgroups per
-    // CU (1.5-3.7% faster than two, and equal to or up to 3.3% faster than
-    // 64-key tiles at two); the causal kernel spills at three and keeps two.
-    entry_dma<128, 32, 4, 2, 3, false, false>(), entry_dma<128, 32, 4, 2, 2, false, true>(),
-    entry_dma<128, 32, 4, 2, 3, true, false>(), entry_dma<128, 32, 4, 2, 2, true, true>(),
-    // D <= 64 is softmax (VALU) bound, and a single wave issues VALU work
-    // well below the SIMD's rate: more resident waves fill the gaps.  D = 64
-    // default: 64-key tiles, whose 32 KB of LDS and <= 168 registers let three
-    // workgroups share a CU (0.7-7.7% faster than 128-key tiles at two, on
-    // every D = 64 workload measured, fp16 and bf16, causal and not).
-    FA_DMA_ENTRIES(64, 64, 4, 2, 3),
-    FA_PP_ENTRIES(64, 64, 4),
-    FA_DMA_ENTRIES(64, 32, 4, 2, 2),
-    FA_DMA_ENTRIES(64, 128, 4, 2, 2),
-    // D = 256: 512 registers per wave (O^T alone is 128), so one workgroup
-    // per CU; 32-key tiles keep S, P and the operand fragments small.  The
-    // 64-key kernels are candidates for the tile sweep.
-    FA_DMA_ENTRIES(256, 32, 4, 2, 1),
-    FA_DMA_ENTRIES(256, 64, 4, 2, 1),
-    // D = 32: four workgroups per CU when causal (8-9% faster than two);
-    // non-causal measured 1.7% slower at four, so it keeps two.
-    entry_dma<32, 64, 4, 2, 2, false, false>(), entry_dma<32, 64, 4, 2, 4, false, true>(),
-    entry_dma<32, 64, 4, 2, 2, true, false>(), entry_dma<32, 64, 4, 2, 4, true, true>(),
-    // D = 16: a 64-key tile is only two DMA instructions; 128 keys give each
-    // wave one.  Three workgroups per CU (4-10% faster than two).
-    FA_DMA_ENTRIES(16, 128, 4, 2, 3),
-    FA_DMA8_ENTRIES(128, 64, 4, 2, 2),
-    // fp8 V at D <= 64: three workgroups per CU (causal 6.7-8.4% faster than
-    // two, non-causal equal).
-    FA_DMA8_ENTRIES(64, 64, 4, 2, 3),
-    FA_DMA8_ENTRIES(256, 64, 4, 2, 1),
-    FA_DMA8_ENTRIES(32, 64, 4, 2, 3),
-    FA_DMA8_ENTRIES(16, 128, 4, 2, 3),
-};
-constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
-
-bool is_supported_head_dim(int d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
-
-bool is_valid_dtype(int dt) {
-  return dt == FA_DTYPE_FP16 || dt == FA_DTYPE_BF16 || dt == FA_DTYPE_FP16_V_E5M2 || dt == FA_DTYPE_BF16_V_E5M2;
-}
-bool v_is_fp8(int dt) { return dt == FA_DTYPE_FP16_V_E5M2 || dt == FA_DTYPE_BF16_V_E5M2; }
-bool out_is_bf16(int dt) { return dt == FA_DTYPE_BF16 || dt == FA_DTYPE_BF16_V_E5M2; }
-// Head dims of the fp8-V kernels.
-bool is_supported_fp8v_head_dim(int d) { return is_supported_head_dim(d); }
-
-// Default (BLOCK_N, waves) per head dim; BLOCK_M = 32 * waves.
-void default_tiling(int D, int dtype, int causal, int *bn, int *nw) {
-  // fp8 V: 64-key tiles (D = 16: 128), one 32x32x64 MFMA per 64 keys and 32
-  // head dims.  16-bit V: 64 keys, except D = 16 (128), D = 256 (32) and
-  // non-causal D = 128 (32, the three-workgroups-per-CU kernel).
-  if (v_is_fp8(dtype))
-    *bn = D == 16 ? 128 : 64;
-  else if (D == 16)
-    *bn = 128;
-  else if (D == 256 || (D == 128 && !causal))
-    *bn = 32;
-  else
-    *bn = 64;
-  *nw = 4;
-}
-
-int find_kernel(int D, int dtype, int causal, int BN, int NW) {
-  for (int i = 0; i < kNumKernels; ++i) {
-    const KernelEntry &e = kKernels[i];
-    if (e.D == D && e.dtype == dtype && e.causal == causal && e.BN == BN && e.NW == NW) return i;
-  }
-  return -1;
-}
-
-struct Plan {
-  int kernel;
-  int BM, BN, NW;
-  int n_mtiles;
-  int64_t total_tiles;  // (head, m-tile) tiles
-  int grid;
-  int split_tiles;      // KV tiles per split-KV run (0: no split)
-};
-
-constexpr int kMaxKvSplits = 64;
-
-// CUs of an MI355X; fa_fwd asks the device, the host-only calls assume this.
-constexpr int kDefaultCuCount = 256;
-
-int make_plan(const fa_fwd_params *p, Plan *out, int cu_count = kDefaultCuCount, int splits = 1) {
-  int bn, nw;
-  if (p->block_m == 0 && p->block_n == 0) {
-    default_tiling(p->D, p->dtype, p->causal, &bn, &nw);
+template <int I>
+KernelFn kernel_fn() {
+  constexpr KernelMeta m = kKernelMeta[I];
+  constexpr bool bf16 = out_is_bf16(m.dtype), v8 = v_is_fp8(m.dtype), causal = m.causal != 0;
+  if constexpr (m.kind == kPingPong) {
+    static_assert(m.NW == Cfg3<m.D, m.BN, m.stages>::NW, "ping-pong workgroup size");
+    static_assert(Cfg3<m.D, m.BN, m.stages>::LDS_BYTES == kernel_lds_bytes(m), "LDS bytes");
+    return fa_fwd_pp_kernel<m.D, m.BN, m.stages, bf16, causal>;
   } else {
-    if (p->block_m <= 0 || p->block_n <= 0 || p->block_m % 32 != 0) return FA_ERR_TILING;
-    bn = p->block_n;
-    nw = p->block_m / 32;
+    static_assert(Cfg2<m.D, m.BN, m.NW, m.stages, m.wg_per_cu, v8>::LDS_BYTES == kernel_lds_bytes(m), "LDS bytes");
+    return fa_fwd_dma_kernel<m.D, m.BN, m.NW, m.stages, m.wg_per_cu, bf16, causal, v8>;
   }
-  const int kid = find_kernel(p->D, p->dtype, p->causal ? 1 : 0, bn, nw);
-  if (kid < 0) return FA_ERR_TILING;
-  out->kernel = kid;
-  out->BN = bn;
-  out->NW = nw;
-  out->BM = 32 * nw;
-  out->n_mtiles = (p->Sq + out->BM - 1) / out->BM;
-  out->total_tiles = (int64_t)out->n_mtiles * p->B * p->H;
-  if (out->total_tiles > INT32_MAX) return FA_ERR_SHAPE;
-  // Persistent grid: as many workgroups as fit on the GPU at once (each
-  // kernel runs two waves per SIMD, so 8 / NW workgroups per CU), pulling
-  // tiles from the tile queues; PERSISTENT_PROGRAMS (num_programs) overrides
-  // the count.
-  const int64_t kv_tiles = ((int64_t)p->Sk + bn - 1) / bn;
-  out->split_tiles = splits > 1 ? (int)((kv_tiles + splits - 1) / splits) : 0;
-  const int64_t units = out->total_tiles * (splits > 1 ? splits : 1);
-  if (units > INT32_MAX) return FA_ERR_SHAPE;
-  int64_t grid = (int64_t)kKernels[kid].wg_per_cu * (cu_count > 0 ? cu_count : kDefaultCuCount);
-  if (p->num_programs > 0) grid = p->num_programs;
-  if (grid > units) grid = units;
-  out->grid = (int)grid;
-  return FA_OK;
 }
+
+template <int... I>
+struct KernelFnTable {
+  const KernelFn fns[sizeof...(I)] = {kernel_fn<I>()...};
+};
+template <int... I>
+KernelFnTable<I...> make_kernel_fn_table(std::integer_sequence<int, I...>);
+const decltype(make_kernel_fn_table(std::make_integer_sequence<int, kNumKernels>{})) kKernelFns{};
 
 // Per-device address of g_tile_queues (hipGetSymbolAddress with the device
 // current), and the launch sequence that picks the queue slot.
@@ -1654,8 +1529,6 @@ int device_cu_count(int device) {
   }
   return n;
 }
-
-bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 }  // namespace
 
@@ -1696,14 +1569,6 @@ static uint32_t *const g_timing_buffer = nullptr;
 
 namespace {
 
-// Workspace of a split-KV launch: partial O, then (256-byte aligned) LSE.
-int64_t split_part_o_bytes(const fa_fwd_params *p, int splits) {
-  return (((int64_t)splits * p->B * p->H * p->Sq * p->D * 4) + 255) / 256 * 256;
-}
-int64_t split_workspace_bytes(const fa_fwd_params *p, int splits) {
-  return split_part_o_bytes(p, splits) + (int64_t)splits * p->B * p->H * p->Sq * 4;
-}
-
 int launch(const fa_fwd_params *p, void *hip_stream, int splits, void *workspace, int64_t workspace_bytes) {
   const int rc = fa_validate(p);
   if (rc != FA_OK) return rc;
@@ -1713,12 +1578,13 @@ int launch(const fa_fwd_params *p, void *hip_stream, int splits, void *workspace
   Plan plan;
   const int prc = make_plan(p, &plan, cu_count, splits);
   if (prc != FA_OK) return prc;
-  const KernelEntry &e = kKernels[plan.kernel];
+  const KernelMeta &e = kKernelMeta[plan.kernel];
   if (splits > 1) {
     if (!e.splittable) return FA_ERR_TILING;
     if (workspace == nullptr) return FA_ERR_NULL;
     if (((uintptr_t)workspace & 255u) != 0) return FA_ERR_ALIGN;
-    if (workspace_bytes < split_workspace_bytes(p, splits)) return FA_ERR_SHAPE;
+    const int64_t need = split_workspace_bytes(p, splits);
+    if (need < 0 || workspace_bytes < need) return FA_ERR_SHAPE;
   }
 
   KernelArgs a;
@@ -1781,7 +1647,7 @@ int launch(const fa_fwd_params *p, void *hip_stream, int splits, void *workspace
   a.c = c;
   a.timing = g_timing_buffer;
 
-  hipLaunchKernelGGL(e.fn, dim3(plan.grid), dim3(64 * e.NW), 0, stream, a);
+  hipLaunchKernelGGL(kKernelFns.fns[plan.kernel], dim3(plan.grid), dim3(64 * e.NW), 0, stream, a);
   if (hipGetLastError() != hipSuccess) return FA_ERR_LAUNCH;
   if (splits > 1) {
     MergeArgs m;
@@ -1807,108 +1673,7 @@ int launch(const fa_fwd_params *p, void *hip_stream, int splits, void *workspace
 
 extern "C" {
 
-int fa_abi_version(void) { return FA_ABI_VERSION; }
-
-const char *fa_error_string(int code) {
-  switch (code) {
-    case FA_OK: return "ok";
-    case FA_ERR_NULL: return "a required tensor pointer is NULL";
-    case FA_ERR_SHAPE: return "invalid shape (negative size, Sq>0 with Sk==0, or too many tiles)";
-    case FA_ERR_HEAD_DIM: return "HEAD_DIM is not one of 16, 32, 64, 128, 256";
-    case FA_ERR_DTYPE: return "dtype must be fp16 or bf16 (optionally with fp8-e5m2 V)";
-    case FA_ERR_STRIDE: return "the head-dim stride must be 1 and the other strides multiples of 8 elements (16 for an fp8 V)";
-    case FA_ERR_ALIGN: return "tensor base pointers must be 16-byte aligned";
-    case FA_ERR_TILING: return "unsupported BLOCK_M/BLOCK_N combination";
-    case FA_ERR_SCALE: return "sm_scale must be finite";
-    case FA_ERR_GRID: return "the persistent program count must be >= 0";
-    case FA_ERR_SCRATCH: return "the split-KV partial results exceed the library's static scratch buffer (FA_STATIC_SCRATCH_BYTES)";
-    case FA_ERR_LAUNCH: return "the HIP runtime rejected the kernel launch";
-    default: return "unknown fa_fwd status";
-  }
-}
-
-int fa_validate(const fa_fwd_params *p) {
-  if (p == nullptr) return FA_ERR_NULL;
-  if (p->B < 0 || p->H < 0 || p->Sq < 0 || p->Sk < 0 || p->D <= 0) return FA_ERR_SHAPE;
-  if (p->Sq > 0 && p->Sk == 0 && p->B > 0 && p->H > 0) return FA_ERR_SHAPE;
-  if (!is_supported_head_dim(p->D)) return FA_ERR_HEAD_DIM;
-  if (!is_valid_dtype(p->dtype)) return FA_ERR_DTYPE;
-  if (v_is_fp8(p->dtype) && !is_supported_fp8v_head_dim(p->D)) return FA_ERR_HEAD_DIM;
-  if (!(p->sm_scale == p->sm_scale) || isinf(p->sm_scale)) return FA_ERR_SCALE;
-  if (p->num_programs < 0) return FA_ERR_GRID;
-  if ((p->block_m == 0) != (p->block_n == 0)) return FA_ERR_TILING;
-  const bool empty = p->B == 0 || p->H == 0 || p->Sq == 0;
-  if (empty) return FA_OK;
-  if (p->q == nullptr || p->k == nullptr || p->v == nullptr || p->o == nullptr) return FA_ERR_NULL;
-  const int64_t *st[4] = {p->q_stride, p->k_stride, p->v_stride, p->o_stride};
-  const int64_t rows[4] = {p->Sq, p->Sk, p->Sk, p->Sq};
-  for (int t = 0; t < 4; ++t) {
-    // 16-byte rows: strides in multiples of 8 16-bit or 16 fp8 elements.
-    const int64_t align = (t == 2 && v_is_fp8(p->dtype)) ? 16 : 8;
-    if (st[t][3] != 1) return FA_ERR_STRIDE;
-    for (int i = 0; i < 3; ++i)
-      if (st[t][i] < 0 || st[t][i] % align != 0) return FA_ERR_STRIDE;
-    if (rows[t] > 1 && st[t][2] < p->D) return FA_ERR_STRIDE;
-    // Buffer offsets inside one (b, h) slice are 32-bit: keep the slice, plus
-    // the rows past its end that a last partial m-tile or the DMAs issued past
-    // the last KV tile address, below 2 GiB.
-    if ((rows[t] + kRowMargin) * (st[t][2] > p->D ? st[t][2] : p->D) * 2 >= ((int64_t)1 << 31))
-      return FA_ERR_SHAPE;
-  }
-  if ((int64_t)p->Sq * 4 >= ((int64_t)1 << 31)) return FA_ERR_SHAPE;
-  if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o)) return FA_ERR_ALIGN;
-  if (p->lse != nullptr && ((uintptr_t)p->lse & 3u) != 0) return FA_ERR_ALIGN;
-  Plan plan;
-  return make_plan(p, &plan);
-}
-
-int fa_query_config(const fa_fwd_params *p, int32_t out[FA_CFG_COUNT]) {
-  if (p == nullptr || out == nullptr) return FA_ERR_NULL;
-  if (p->B < 0 || p->H < 0 || p->Sq < 0 || p->Sk < 0) return FA_ERR_SHAPE;
-  if (!is_supported_head_dim(p->D)) return FA_ERR_HEAD_DIM;
-  if (!is_valid_dtype(p->dtype)) return FA_ERR_DTYPE;
-  if (v_is_fp8(p->dtype) && !is_supported_fp8v_head_dim(p->D)) return FA_ERR_HEAD_DIM;
-  if ((p->block_m == 0) != (p->block_n == 0)) return FA_ERR_TILING;
-  if (p->num_programs < 0) return FA_ERR_GRID;
-  Plan plan;
-  const int rc = make_plan(p, &plan);
-  if (rc != FA_OK) return rc;
-  out[FA_CFG_BLOCK_M] = plan.BM;
-  out[FA_CFG_BLOCK_N] = plan.BN;
-  out[FA_CFG_WAVES] = plan.NW;
-  out[FA_CFG_GRID] = plan.grid;
-  out[FA_CFG_TOTAL_TILES] = (int32_t)plan.total_tiles;
-  out[FA_CFG_LDS_BYTES] = kKernels[plan.kernel].lds_bytes;
-  out[FA_CFG_STAGE] = p->causal ? 3 : 1;
-  out[FA_CFG_KERNEL_ID] = plan.kernel;
-  return FA_OK;
-}
-
-int fa_num_kernels(void) { return kNumKernels; }
-
-int fa_params_size(void) { return (int)sizeof(fa_fwd_params); }
-
-int fa_kernel_info(int index, int32_t out[6]) {
-  if (out == nullptr) return FA_ERR_NULL;
-  if (index < 0 || index >= kNumKernels) return FA_ERR_TILING;
-  const KernelEntry &e = kKernels[index];
-  out[0] = e.D;
-  out[1] = e.dtype;
-  out[2] = e.causal;
-  out[3] = 32 * e.NW;
-  out[4] = e.BN;
-  out[5] = e.NW;
-  return FA_OK;
-}
-
 int fa_fwd(const fa_fwd_params *p, void *hip_stream) { return launch(p, hip_stream, 1, nullptr, 0); }
-
-int64_t fa_split_workspace_bytes(const fa_fwd_params *p, int32_t kv_splits) {
-  if (p == nullptr) return FA_ERR_NULL;
-  if (kv_splits < 1 || kv_splits > kMaxKvSplits) return FA_ERR_GRID;
-  if (p->B < 0 || p->H < 0 || p->Sq < 0 || p->D <= 0) return FA_ERR_SHAPE;
-  return kv_splits == 1 ? 0 : split_workspace_bytes(p, kv_splits);
-}
 
 int fa_fwd_split(const fa_fwd_params *p, int32_t kv_splits, void *workspace, int64_t workspace_bytes,
                  void *hip_stream) {
@@ -1921,36 +1686,13 @@ int fa_fwd_split_static(const fa_fwd_params *p, int32_t kv_splits, void *hip_str
   const int rc = fa_validate(p);
   if (rc != FA_OK) return rc;
   if (kv_splits == 1) return launch(p, hip_stream, 1, nullptr, 0);
-  if (split_workspace_bytes(p, kv_splits) > (int64_t)FA_STATIC_SCRATCH_BYTES) return FA_ERR_SCRATCH;
+  const int64_t need = split_workspace_bytes(p, kv_splits);
+  if (need < 0 || need > (int64_t)FA_STATIC_SCRATCH_BYTES) return FA_ERR_SCRATCH;
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess) return FA_ERR_LAUNCH;
   char *base = static_scratch_base(device);
   if (base == nullptr) return FA_ERR_LAUNCH;
   return launch(p, hip_stream, kv_splits, base, (int64_t)FA_STATIC_SCRATCH_BYTES);
-}
-
-int32_t fa_default_kv_splits(const fa_fwd_params *p) {
-  // Shape-only (no pointer or stride checks): usable before tensors exist.
-  if (p == nullptr || p->B <= 0 || p->H <= 0 || p->Sq <= 0 || p->Sk <= 0) return 1;
-  if (!is_supported_head_dim(p->D) || !is_valid_dtype(p->dtype)) return 1;
-  Plan plan;
-  if (make_plan(p, &plan) != FA_OK) return 1;
-  const KernelEntry &e = kKernels[plan.kernel];
-  if (!e.splittable) return 1;
-  // Split only a grid that would leave most workgroup slots empty, and only
-  // into runs of at least 8 KV tiles and 512 keys (the merge costs an extra
-  // HBM pass).
-  // Slots count at most two workgroups per CU: a third or fourth one only
-  // fills VALU issue gaps, and splitting further to occupy it cost more in
-  // merge work (B2 H4 S4096 D16 causal: 3 splits 8% slower than 2).
-  const int64_t slots = (int64_t)(e.wg_per_cu < 2 ? e.wg_per_cu : 2) * kDefaultCuCount;
-  if (plan.total_tiles * 2 > slots) return 1;
-  const int64_t kv_tiles = ((int64_t)p->Sk + plan.BN - 1) / plan.BN;
-  int64_t splits = (slots + plan.total_tiles - 1) / plan.total_tiles;
-  const int64_t min_run = 512 / plan.BN > 8 ? 512 / plan.BN : 8;  // KV tiles
-  if (splits > kv_tiles / min_run) splits = kv_tiles / min_run;
-  if (splits > kMaxKvSplits) splits = kMaxKvSplits;
-  return splits > 1 ? (int32_t)splits : 1;
 }
 
 }  // extern "C"

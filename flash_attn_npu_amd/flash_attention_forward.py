@@ -51,7 +51,8 @@ REFERENCE_HEAD_DIMS = (16, 32, 64, 128, 256)
 
 # BEGIN AUTO-TUNED DEFAULT TILING PRESETS
 # (Z, H, N_CTX, HEAD_DIM, causal) -> (BLOCK_M, BLOCK_N), rewritten by
-# python -m flash_attn_npu_amd.tune from gfx950 sweeps.
+# python -m flash_attn_npu_amd.tune from gfx950 sweeps: float16 inputs here,
+# bfloat16 inputs in DEFAULT_TILING_PRESETS_BF16.
 DEFAULT_TILING_PRESETS = {
     (128, 8, 1024, 128, True): (128, 32),
     (128, 8, 1024, 256, True): (128, 32),
@@ -59,6 +60,8 @@ DEFAULT_TILING_PRESETS = {
     (128, 8, 2048, 256, False): (128, 32),
     (128, 8, 4096, 128, False): (128, 32),
     (128, 8, 8192, 64, False): (128, 128),
+}
+DEFAULT_TILING_PRESETS_BF16 = {
 }
 # END AUTO-TUNED DEFAULT TILING PRESETS
 
@@ -151,6 +154,10 @@ def _load_library():
     lib.fa_kernel_info.restype = ctypes.c_int
     lib.fa_params_size.argtypes = []
     lib.fa_params_size.restype = ctypes.c_int
+    lib.fa_kernel_wg_per_cu.argtypes = [ctypes.c_int]
+    lib.fa_kernel_wg_per_cu.restype = ctypes.c_int
+    lib.fa_build_id.argtypes = []
+    lib.fa_build_id.restype = ctypes.c_char_p
     lib.fa_split_workspace_bytes.argtypes = [P, ctypes.c_int32]
     lib.fa_split_workspace_bytes.restype = ctypes.c_int64
     lib.fa_fwd_split.argtypes = [P, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
@@ -175,14 +182,18 @@ def _check(rc: int, what: str) -> None:
 
 
 def kernel_table():
-    """All kernel instances in the library: dicts of D, dtype, causal, BLOCK_M, BLOCK_N, waves."""
+    """All kernel instances in the library: dicts of D, dtype, causal, BLOCK_M, BLOCK_N,
+    waves and resident workgroups per CU."""
     lib = _load_library()
     out = (ctypes.c_int32 * 6)()
     rows = []
     for i in range(lib.fa_num_kernels()):
         _check(lib.fa_kernel_info(i, out), "fa_kernel_info")
+        wg = lib.fa_kernel_wg_per_cu(i)
+        _check(wg if wg < 0 else 0, "fa_kernel_wg_per_cu")
         rows.append({"HEAD_DIM": out[0], "dtype": _DTYPE_NAMES.get(out[1], str(out[1])),
-                     "causal": bool(out[2]), "BLOCK_M": out[3], "BLOCK_N": out[4], "waves": out[5]})
+                     "causal": bool(out[2]), "BLOCK_M": out[3], "BLOCK_N": out[4], "waves": out[5],
+                     "wg_per_cu": wg})
     return rows
 
 
@@ -237,35 +248,43 @@ def _query_config(z, h, n_ctx, head_dim, causal, bm=0, bn=0, dtype=torch.float16
 _FALLBACK_TILING = {}
 
 
-def _default_tiling(z, h, n_ctx, head_dim, causal):
-    """Preset for this exact shape, else the library's gfx950 default."""
+def _presets_for(dtype):
+    """The preset table of an input dtype: the reference's table for float16, a second
+    one for bfloat16 (each filled by a sweep in that dtype)."""
+    return DEFAULT_TILING_PRESETS_BF16 if dtype == torch.bfloat16 else DEFAULT_TILING_PRESETS
+
+
+def _default_tiling(z, h, n_ctx, head_dim, causal, dtype=torch.float16):
+    """Preset for this exact shape and dtype, else the library's gfx950 default."""
     key = (z, h, n_ctx, head_dim, causal)
-    preset = DEFAULT_TILING_PRESETS.get(key)
+    preset = _presets_for(dtype).get(key)
     if preset is not None:
         return preset
-    tiling = _FALLBACK_TILING.get(key)
+    fkey = key + (dtype,)
+    tiling = _FALLBACK_TILING.get(fkey)
     if tiling is None:
-        cfg = _query_config(z, h, n_ctx, head_dim, causal)
-        tiling = _FALLBACK_TILING[key] = (cfg[0], cfg[1])
+        cfg = _query_config(z, h, n_ctx, head_dim, causal, dtype=dtype)
+        tiling = _FALLBACK_TILING[fkey] = (cfg[0], cfg[1])
     return tiling
 
 
-def get_tiling(z, h, n_ctx, head_dim, causal):
-    return _default_tiling(z, h, n_ctx, head_dim, causal)
+def get_tiling(z, h, n_ctx, head_dim, causal, dtype=torch.float16):
+    return _default_tiling(z, h, n_ctx, head_dim, causal, dtype)
 
 
-def get_tiling_source(z, h, n_ctx, head_dim, causal):
-    if (z, h, n_ctx, head_dim, causal) in DEFAULT_TILING_PRESETS:
+def get_tiling_source(z, h, n_ctx, head_dim, causal, dtype=torch.float16):
+    if (z, h, n_ctx, head_dim, causal) in _presets_for(dtype):
         return "preset"
     return "fallback"
 
 
-def _resolve_tiling(z, h, n_ctx, head_dim, causal, bm=None, bn=None):
+def _resolve_tiling(z, h, n_ctx, head_dim, causal, bm=None, bn=None, dtype=torch.float16):
     if (bm is None) != (bn is None):
         raise ValueError("BM and BN must be provided together")
     if bm is not None:
         return bm, bn, "override"
-    return (*get_tiling(z, h, n_ctx, head_dim, causal), get_tiling_source(z, h, n_ctx, head_dim, causal))
+    return (*get_tiling(z, h, n_ctx, head_dim, causal, dtype),
+            get_tiling_source(z, h, n_ctx, head_dim, causal, dtype))
 
 
 def _describe_runtime(z, h, n_ctx, head_dim, causal, bm=None, bn=None, dtype=torch.float16, v_dtype=None):
@@ -274,7 +293,7 @@ def _describe_runtime(z, h, n_ctx, head_dim, causal, bm=None, bn=None, dtype=tor
     dtype is the q/k/o element type and v_dtype V's (None: the same; float8_e5m2 selects
     the fp8-V kernels, as _launch_kernel does).
     """
-    block_m, block_n, tiling_source = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn)
+    block_m, block_n, tiling_source = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn, dtype)
     fp8_v = v_dtype == FP8_V_DTYPE
     if fp8_v and tiling_source != "override":
         block_m, block_n = fp8_v_tiling(head_dim)
@@ -395,7 +414,7 @@ def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
     _validate_inputs(q, k, v)
     z, h, n_ctx, head_dim = q.shape
     causal = bool(causal)
-    bm, bn, source = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn)
+    bm, bn, source = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn, q.dtype)
     if v.dtype == FP8_V_DTYPE and source != "override":
         bm, bn = fp8_v_tiling(head_dim)  # the fp8-V kernels' one tiling; presets are for 16-bit V
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
@@ -474,6 +493,7 @@ __all__ = [
     "RESULT_DIR_NAME",
     "PROFILE_OP_NAME",
     "DEFAULT_TILING_PRESETS",
+    "DEFAULT_TILING_PRESETS_BF16",
     "get_tiling",
     "get_tiling_source",
     "attention",

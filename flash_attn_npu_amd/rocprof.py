@@ -42,7 +42,8 @@ METRIC_PLAN = {
     "LDS": ["SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_WAIT_INST_LDS",
             "SQ_ACTIVE_INST_LDS", "SQ_VALU_MFMA_COEXEC_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY"],
     "L2": ["TCC_HIT_sum", "TCC_MISS_sum"],
-    "HBMRead": ["FETCH_SIZE"],
+    # FETCH_SIZE (3 TCC counters) and the memory-side read request count (1 more).
+    "HBMRead": ["FETCH_SIZE", "TCC_EA0_RDREQ_DRAM_sum"],
     "HBMWrite": ["WRITE_SIZE"],
 }
 
@@ -62,8 +63,11 @@ def _is_target(name: str, op: str) -> bool:
 
 
 def _is_copy(name: str) -> bool:
+    """The calibration copy (torch's device copy, a copy kernel or the runtime's
+    copyBuffer blit); fills and other elementwise kernels of the same process
+    read nothing and must not dilute the factor."""
     low = name.lower()
-    return "copy" in low or "elementwise" in low
+    return "copy" in low and "fill" not in low
 
 
 def _find(root: Path, suffix: str):
@@ -124,6 +128,12 @@ def summarize_pass(pass_dir: Path, op: str = PROFILE_OP_NAME) -> dict:
                 factor = COPY_BYTES / (statistics.mean(copy_counters[cname]) * 1024.0)
                 k[f"{cname}_copy_factor"] = factor
             k[label] = k[cname] * 1024.0 * factor
+    if "TCC_EA0_RDREQ_DRAM_sum" in k and copy_counters.get("TCC_EA0_RDREQ_DRAM_sum"):
+        # Second read figure: memory-side read requests times the bytes per
+        # request of the calibration copy.
+        per_req = COPY_BYTES / statistics.mean(copy_counters["TCC_EA0_RDREQ_DRAM_sum"])
+        k["TCC_EA0_RDREQ_DRAM_bytes_per_req"] = per_req
+        k["hbm_read_bytes_by_requests"] = k["TCC_EA0_RDREQ_DRAM_sum"] * per_req
     if "TCC_HIT_sum" in k and "TCC_MISS_sum" in k:
         tot = k["TCC_HIT_sum"] + k["TCC_MISS_sum"]
         entry["l2"] = {"l2_count": 1.0, "Hit Rate": k["TCC_HIT_sum"] / tot if tot else None}
@@ -131,6 +141,60 @@ def summarize_pass(pass_dir: Path, op: str = PROFILE_OP_NAME) -> dict:
     entry["kernel_columns"] = [c for c in k if c != "kernel_count"]
     entry["api"] = {"launch": {"Count": entry["op"].get("Count")}}
     return entry
+
+
+def _dispatch_key(row: dict, index: int):
+    for col in ("Dispatch_Id", "Correlation_Id"):
+        val = row.get(col)
+        if val not in (None, ""):
+            return int(float(val))
+    return index
+
+
+def read_dispatches(pass_dir: Path, match) -> list[dict]:
+    """Per-dispatch records of one pass, in dispatch order, for kernels whose name
+    satisfies `match(name)`: {"name", "duration_us" (kernel-trace passes),
+    "counters": {counter: value}}.
+
+    Counter rows are grouped by Dispatch_Id (rocprofv3 writes one row per
+    dispatch and counter); a file without that column is grouped by
+    occurrence (the i-th value of a counter belongs to the i-th dispatch).
+    """
+    by_id: dict[int, dict] = {}
+    for tr in _find(Path(pass_dir), "kernel_trace.csv"):
+        for i, r in enumerate(_read_csv(tr)):
+            if not match(r["Kernel_Name"]):
+                continue
+            rec = by_id.setdefault(_dispatch_key(r, i), {"name": r["Kernel_Name"], "counters": {}})
+            rec["duration_us"] = (float(r["End_Timestamp"]) - float(r["Start_Timestamp"])) / 1e3
+    for cc in _find(Path(pass_dir), "counter_collection.csv"):
+        seen: dict[str, int] = {}
+        for r in _read_csv(cc):
+            if not match(r["Kernel_Name"]):
+                continue
+            name = r["Counter_Name"]
+            if "Dispatch_Id" in r or "Correlation_Id" in r:
+                key = _dispatch_key(r, 0)
+            else:
+                key = seen.get(name, 0)
+                seen[name] = key + 1
+            rec = by_id.setdefault(key, {"name": r["Kernel_Name"], "counters": {}})
+            rec["counters"][name] = rec["counters"].get(name, 0.0) + float(r["Counter_Value"])
+    return [by_id[k] for k in sorted(by_id)]
+
+
+def copy_factors(pass_dir: Path) -> dict:
+    """Copy calibration of a pass, from the plain device copy in the same process:
+    for FETCH_SIZE / WRITE_SIZE (KiB) the factor COPY_BYTES / reading, for the
+    memory-side read request count the bytes per request."""
+    out = {}
+    for rec in read_dispatches(pass_dir, _is_copy):
+        for name, val in rec["counters"].items():
+            if name in ("FETCH_SIZE", "WRITE_SIZE") and val > 0:
+                out.setdefault(name, []).append(COPY_BYTES / (val * 1024.0))
+            elif name == "TCC_EA0_RDREQ_DRAM_sum" and val > 0:
+                out.setdefault(name, []).append(COPY_BYTES / val)
+    return {k: statistics.mean(v) for k, v in out.items()}
 
 
 def write_profile_summary_files(root: Path, summary_by_metric: dict):

@@ -142,6 +142,18 @@ int fa_abi_version(void);
 int fa_num_kernels(void);
 int fa_kernel_info(int index, int32_t out[6]);
 
+/* Resident workgroups per CU of kernel entry `index` (what its registers and
+ * LDS allow; the persistent grid launches that many per CU), or FA_ERR_TILING
+ * for an index out of range.  Host-only; the tile sweep records it with each
+ * (BLOCK_M, BLOCK_N) candidate. */
+int fa_kernel_wg_per_cu(int index);
+
+/* Hash of the sources the library was compiled from (kernel source and this
+ * header), as the build recipe computed it, or "unknown" for a build made
+ * without it.  Host-only; lets a caller detect a library older than its
+ * sources. */
+const char *fa_build_id(void);
+
 /* sizeof(fa_fwd_params) as compiled into the library, so a foreign binding
  * (ctypes, cffi) can check its struct layout before the first call. */
 int fa_params_size(void);

@@ -51,6 +51,32 @@ def test_exported_symbols_in_dynamic_table():
     assert set(header_functions()) <= exported
 
 
+def test_library_is_built_from_the_current_sources(lib):
+    """The loaded library carries the hash of the kernel source and header it was
+    compiled from; a library older than its sources fails here (rebuild it)."""
+    from flash_attn_npu_amd.build import source_hash
+    assert lib.fa_build_id().decode() == source_hash(), "stale libfa_mi355x.so: rebuild it"
+
+
+def test_kernel_workgroups_per_cu(lib):
+    table = fa.kernel_table()
+    assert len(table) == lib.fa_num_kernels()
+    assert lib.fa_kernel_wg_per_cu(-1) == lib.fa_kernel_wg_per_cu(len(table)) == -7
+    for i, row in enumerate(table):
+        assert 1 <= row["wg_per_cu"] <= 4
+        # LDS bytes of one workgroup times the resident count fit one CU's 160 KB.
+        p = _params(shape=(64, 64, 4096, row["HEAD_DIM"]), dtype={"float16": 0, "bfloat16": 1,
+                    "float16+float8_e5m2_v": 2, "bfloat16+float8_e5m2_v": 3}[row["dtype"]],
+                    causal=int(row["causal"]))
+        p.block_m, p.block_n = row["BLOCK_M"], row["BLOCK_N"]
+        out = (ctypes.c_int32 * fa.FA_CFG_COUNT)()
+        assert lib.fa_query_config(ctypes.byref(p), out) == 0
+        assert out[7] == i  # every entry is reachable by its own key
+        assert out[5] * row["wg_per_cu"] <= 160 * 1024
+        # The persistent grid is the resident capacity of the 256 CUs.
+        assert out[3] == row["wg_per_cu"] * 256
+
+
 def test_abi_version_and_struct_layout(lib):
     assert lib.fa_abi_version() == 1
     assert lib.fa_params_size() == ctypes.sizeof(fa.FaFwdParams) == 216
@@ -242,11 +268,28 @@ def test_tiling_resolution(monkeypatch):
     assert fa.get_tiling_source(2, 3, 4097, 128, True) == "fallback"
 
 
+def test_presets_are_per_dtype(monkeypatch):
+    """A bfloat16 sweep's presets serve bfloat16 calls only, and the float16 table
+    (the reference's DEFAULT_TILING_PRESETS) float16 calls only."""
+    key = (2, 3, 4096, 128, True)
+    monkeypatch.setitem(fa.DEFAULT_TILING_PRESETS, key, (256, 64))
+    monkeypatch.setitem(fa.DEFAULT_TILING_PRESETS_BF16, key, (128, 32))
+    assert fa.get_tiling(*key) == (256, 64)
+    assert fa.get_tiling(*key, dtype=torch.float16) == (256, 64)
+    assert fa.get_tiling(*key, dtype=torch.bfloat16) == (128, 32)
+    assert fa._resolve_tiling(*key, dtype=torch.bfloat16) == (128, 32, "preset")
+    assert fa._describe_runtime(*key, dtype=torch.bfloat16)["selected_config"] == {"BLOCK_M": 128, "BLOCK_N": 32}
+    assert fa._describe_runtime(*key)["selected_config"] == {"BLOCK_M": 256, "BLOCK_N": 64}
+    monkeypatch.delitem(fa.DEFAULT_TILING_PRESETS_BF16, key)
+    assert fa.get_tiling_source(*key, dtype=torch.bfloat16) == "fallback"
+    assert fa.get_tiling(*key, dtype=torch.bfloat16) == tuple(fa._query_config(*key, dtype=torch.bfloat16)[:2])
+
+
 def test_fallback_tiling_cached_per_shape(monkeypatch):
     """The library's default tiling is asked once per shape and the cached
     answer is the library's; a preset for the shape still wins."""
     key = (3, 5, 777, 64, True)
-    fa._FALLBACK_TILING.pop(key, None)
+    fa._FALLBACK_TILING.pop(key + (torch.float16,), None)
     want = tuple(fa._query_config(*key)[:2])
     calls = []
     real = fa._query_config
