@@ -54,14 +54,25 @@ REFERENCE_HEAD_DIMS = (16, 32, 64, 128, 256)
 # python -m flash_attn_npu_amd.tune from gfx950 sweeps: float16 inputs here,
 # bfloat16 inputs in DEFAULT_TILING_PRESETS_BF16.
 DEFAULT_TILING_PRESETS = {
-    (128, 8, 1024, 128, True): (128, 32),
+    (1, 8, 512, 64, False): (128, 128),
+    (16, 16, 1024, 64, False): (128, 64),
+    (128, 8, 1024, 128, True): (128, 64),
     (128, 8, 1024, 256, True): (128, 32),
-    (128, 8, 2048, 128, True): (128, 32),
+    (128, 8, 2048, 128, True): (128, 64),
     (128, 8, 2048, 256, False): (128, 32),
-    (128, 8, 4096, 128, False): (128, 32),
-    (128, 8, 8192, 64, False): (128, 128),
+    (128, 8, 4096, 128, False): (128, 64),
+    (128, 8, 8192, 64, False): (128, 64),
 }
 DEFAULT_TILING_PRESETS_BF16 = {
+    (2, 16, 8192, 128, True): (128, 64),
+    (4, 32, 2048, 128, True): (128, 64),
+    (8, 32, 3000, 128, True): (128, 64),
+    (128, 8, 1024, 128, True): (128, 64),
+    (128, 8, 1024, 256, True): (128, 32),
+    (128, 8, 2048, 128, True): (128, 64),
+    (128, 8, 2048, 256, False): (128, 32),
+    (128, 8, 4096, 128, False): (128, 32),
+    (128, 8, 8192, 64, False): (128, 64),
 }
 # END AUTO-TUNED DEFAULT TILING PRESETS
 

@@ -12,7 +12,11 @@ the headline number:
   * `--rounds` rounds; in each, every candidate gets 2 untimed launches and
     then `--launches` (>= 20) back-to-back launches between two HIP events on
     the launch stream; candidates rotate their order from round to round;
-  * a candidate's time is the median over rounds of its per-launch average.
+  * a candidate's time is the median over rounds of its per-launch average;
+  * when the fastest candidate's launch is shorter than `--graph-below-us`
+    (40 µs: the host's per-call cost, ~13 µs, then sets the pace of eager
+    launches), the rounds are timed again as replays of HIP graphs that hold
+    `--launches` launches each, so the ranking is by device time.
 
 The winner is re-timed next to the vendor baseline (PyTorch-ROCm fused SDPA,
 as in flash_attn_npu_amd/evaluate.py) both back to back and per call with a
@@ -69,7 +73,7 @@ PRESET_END = "# END AUTO-TUNED DEFAULT TILING PRESETS"
 PACKAGE_DIR = Path(__file__).resolve().parent
 DEFAULT_OUTPUT_JSON = PACKAGE_DIR / "flash_attention_forward_tuned.json"
 DEFAULTS = dict(sm_scale=W.REFERENCE_SM_SCALE, seed=0, warmup_seconds=1.0, rounds=5, launches=20,
-                final_iters=20, tie_pct=1.0)
+                final_iters=20, tie_pct=1.0, graph_below_us=40.0)
 DTYPE_SUFFIX = {torch.float16: "", torch.bfloat16: ":bf16"}
 PROFILE_LAUNCHES = 5  # per profiled configuration and pass; the first is not counted
 
@@ -202,14 +206,50 @@ def percall_us(fn, iters: int):
     return out, {"avg_us": statistics.mean(samples), "min_us": min(samples), "max_us": max(samples)}
 
 
-def time_candidates(fns: dict, rounds: int, launches: int):
-    """Interleaved back-to-back timing: per candidate, the per-round per-launch
-    averages (rotating the order each round so drift hits every candidate)."""
+def graph_per_launch(fn, launches: int):
+    """A callable that replays `launches` calls captured in one HIP graph and
+    returns the µs per launch between two events: the device time of a launch
+    without the host's per-call cost (which back-to-back eager launches of a
+    short kernel cannot hide)."""
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # first use of the allocator pool outside the capture
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(launches):
+                fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+
+    def replay():
+        stream = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / launches
+
+    replay.graph = g
+    return replay
+
+
+def time_candidates(fns: dict, rounds: int, launches: int, graphs: dict | None = None):
+    """Interleaved timing: per candidate, the per-round per-launch averages
+    (rotating the order each round so drift hits every candidate).  Back-to-back
+    eager launches, or replays of `graphs[name]` when given."""
     names = list(fns)
     per = {n: [] for n in names}
     for r in range(rounds):
         order = names[r % len(names):] + names[:r % len(names)]
         for n in order:
+            if graphs is not None:
+                graphs[n]()
+                per[n].append(graphs[n]())
+                continue
             fn = fns[n]
             fn()
             fn()
@@ -246,9 +286,17 @@ def tune_case(module, vendor, case: Case, opts) -> dict:
     default_tag = "{}x{}".format(*library_default(module, case.shape, dtype))
     warm_up(fns.get(default_tag, next(iter(fns.values()))), opts.warmup_seconds)
     per = time_candidates(fns, opts.rounds, opts.launches)
+    timing = "eager"
+    if min(statistics.median(xs) for xs in per.values()) < opts.graph_below_us:
+        # A launch this short is shorter than the host's per-call cost: back-to-back
+        # eager launches then time the host.  Rank the device time of graph replays.
+        graphs = {tag: graph_per_launch(fn, opts.launches) for tag, fn in fns.items()}
+        per = time_candidates(fns, opts.rounds, opts.launches, graphs)
+        timing = "graph"
+        del graphs
     for tag, xs in per.items():
         rows[tag].update(avg_us=statistics.median(xs), min_us=min(xs), max_us=max(xs), rounds_us=xs,
-                         launches_per_round=opts.launches)
+                         launches_per_round=opts.launches, timing=timing)
     viable = sorted((r for r in rows.values() if r.get("avg_us") is not None), key=lambda r: r["avg_us"])
     fastest = viable[0]
     best_row = fastest
@@ -272,7 +320,7 @@ def tune_case(module, vendor, case: Case, opts) -> dict:
     best_fn = fns[best_tag]
     cand_out, pc = percall_us(best_fn, opts.final_iters)
     result = {"Z": z, "H": h, "N_CTX": n, "HEAD_DIM": d, "causal": bool(causal), "dtype": E.dtype_name(dtype),
-              "sm_scale": case.sm_scale, "workload": case.workload, "best_config": best,
+              "sm_scale": case.sm_scale, "workload": case.workload, "best_config": best, "timing": timing,
               "library_default": default_tag, "choice": choice,
               "candidate_avg_us": best_row["avg_us"], "candidate_min_us": best_row["min_us"],
               "candidate_max_us": best_row["max_us"], "percall_avg_us": pc["avg_us"],
@@ -561,6 +609,8 @@ def main(argv=None):
     ap.add_argument("--launches", type=int, default=DEFAULTS["launches"], help="timed launches per round")
     ap.add_argument("--final-iters", type=int, default=DEFAULTS["final_iters"], help="per-call timing iterations")
     ap.add_argument("--tie-pct", type=float, default=DEFAULTS["tie_pct"])
+    ap.add_argument("--graph-below-us", type=float, default=DEFAULTS["graph_below_us"],
+                    help="rank by HIP-graph replays when the fastest eager launch is shorter than this")
     ap.add_argument("--replace-output", action="store_true")
     ap.add_argument("--shape", action="append", help="Z,H,N_CTX,HEAD_DIM,causal (repeatable)")
     ap.add_argument("--skip-apply", action="store_true")
