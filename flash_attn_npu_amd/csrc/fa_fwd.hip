@@ -537,7 +537,6 @@ fa_fwd_dma_kernel(KernelArgs p) {
                            &bh, &mt, &split);
        ++it) {
     unsigned long long next_raw = 0;
-    if (threadIdx.x == 0) next_raw = tq.request();
 #ifdef FA_TIMING
     uint32_t tm_vm = 0, tm_bar = 0, tm_cmp = 0, n_comp = 0, tm_pro = 0, tm_epi0 = 0, tm_dma = 0, tm_idle = 0;
     const uint32_t tm0 = FA_CLK();
@@ -560,6 +559,27 @@ fa_fwd_dma_kernel(KernelArgs p) {
     const int t_begin = split * p.split_tiles;
     const int n_tiles = min((kv_end + BN - 1) / BN, t_begin + p.split_tiles);
     const int wave_last_q = q0w + 31;
+    // Thread 0 takes the next ticket.  When wave 0 has no work in the unit's
+    // last tile (under the causal mask its rows end before that tile's keys,
+    // or they lie past Sq), the request waits for that idle tile: the atomic
+    // returns while the other waves compute it, and units start in ticket
+    // order.  Requested at the unit's start, a ticket stayed reserved for a
+    // whole unit and heavy units taken that way started late (B4 H32 S2048
+    // causal: the workgroups of one queue ended between 114 and 144 us).
+    // Otherwise (every wave computes the last tile; non-causal units are all
+    // alike anyway) it is requested at the unit's start, where its latency
+    // hides behind the first tile's loads; a request inside the tile code
+    // cost the kernels 30 or more registers.
+    // Tiles visible to every query of the workgroup (no mask needed).
+    auto n_full_of = [&](int q0_) __attribute__((always_inline)) {
+      int nf = p.Sk / BN;
+      if (CAUSAL) nf = min(nf, (q0_ + 1) / BN);
+      return min(nf, n_tiles);
+    };
+    const int t_last = n_tiles - 1;
+    const int w0_act = (CAUSAL && OCC >= 2) ? max(n_full_of(q0), min(n_tiles, (q0 + 31) / BN + 1)) : n_tiles;
+    const bool late_ticket = OCC >= 2 && n_tiles > t_begin && (q0 >= p.Sq || w0_act < n_tiles);
+    if (threadIdx.x == 0 && !late_ticket) next_raw = tq.request();
 
     // DMA of KV tile t into stage STG: instruction i < 2*IPW of this wave
     // (K rows for even i, V rows for odd i).  Past the last tile the buffer
@@ -866,9 +886,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
 
     // Tiles visible to every query of the workgroup need no mask.  Each run
     // of tiles steps t in stage pairs (t even -> stage 0).
-    int n_full = p.Sk / BN;
-    if (CAUSAL) n_full = min(n_full, (q0 + 1) / BN);
-    n_full = min(n_full, n_tiles);
+    const int n_full = n_full_of(q0);
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
     int t = t_begin;
@@ -889,6 +907,7 @@ fa_fwd_dma_kernel(KernelArgs p) {
         __syncthreads();
         BufRsrc rk_n, rv_n;
         tile_rsrc(t + 1, &rk_n, &rv_n);
+        if (late_ticket && t == t_last && threadIdx.x == 0) next_raw = tq.request();
         if (t & 1) {
 #pragma unroll
           for (int i = 0; i < C::NDMA; ++i) dma(S0{}, rk_n, rv_n, i);
