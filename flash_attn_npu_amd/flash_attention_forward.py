@@ -417,29 +417,57 @@ def _launch_plan(lib, q, k, v, out, causal, bm, bn, programs, split_env):
     return plan
 
 
+# Calls whose q, k, v the kernel reads in place, keyed by everything the argument checks,
+# the tiling and the launch plan depend on (shapes, strides, dtypes, devices, mask,
+# BM/BN override, the two environment variables): a repeated call goes straight to
+# allocation and launch.  Tensors at a base address that is not 16-byte aligned take
+# the full path (and are copied there).
+_FAST_PLANS = {}
+
+
+def _call_key(q, k, v, causal, bm, bn):
+    env = os.environ
+    return (q.shape, k.shape, v.shape, q.stride(), k.stride(), v.stride(), q.dtype, k.dtype, v.dtype,
+            q.device, k.device, v.device, causal, bm, bn, env.get("PERSISTENT_PROGRAMS"), env.get("KV_SPLITS"))
+
+
 def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
     """Validate, resolve tiling, allocate O/LSE, launch; returns (out, lse).
 
     Same flow and return value as flash_attention_forward.py:1130-1194.
     """
+    causal = bool(causal)
+    key = _call_key(q, k, v, causal, bm, bn)
+    plan = _FAST_PLANS.get(key)
+    if plan is not None and not (q.data_ptr() | k.data_ptr() | v.data_ptr()) & 15:
+        out = torch.empty_like(q)
+        lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
+        _launch(plan, q, k, v, out, lse, sm_scale)
+        return out, lse
     _validate_inputs(q, k, v)
     z, h, n_ctx, head_dim = q.shape
-    causal = bool(causal)
-    bm, bn, source = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn, q.dtype)
+    bm_r, bn_r, source = _resolve_tiling(z, h, n_ctx, head_dim, causal, bm, bn, q.dtype)
     if v.dtype == FP8_V_DTYPE and source != "override":
-        bm, bn = fp8_v_tiling(head_dim)  # the fp8-V kernels' one tiling; presets are for 16-bit V
-    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
-    out = torch.empty_like(q)
+        bm_r, bn_r = fp8_v_tiling(head_dim)  # the fp8-V kernels' one tiling; presets are for 16-bit V
+    qr, kr, vr = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    out = torch.empty_like(qr)
     lse = torch.empty((z, h, n_ctx), device=q.device, dtype=torch.float32)
     if out.numel() == 0:
         return out, lse
-    out = _kernel_ready(out)
+    out_r = _kernel_ready(out)
+    lib = _load_library()
+    plan = _launch_plan(lib, qr, kr, vr, out_r, causal, bm_r, bn_r, _get_persistent_programs(), _get_kv_splits())
+    _launch(plan, qr, kr, vr, out_r, lse, sm_scale)
+    if qr is q and kr is k and vr is v and out_r is out:
+        _FAST_PLANS[key] = plan
+    return out_r, lse
+
+
+def _launch(plan, q, k, v, out, lse, sm_scale):
     sm_scale = float(sm_scale)
     if not math.isfinite(sm_scale):
         raise ValueError("sm_scale must be finite")
-
-    lib = _load_library()
-    plan = _launch_plan(lib, q, k, v, out, causal, bm, bn, _get_persistent_programs(), _get_kv_splits())
+    lib = _LIB
     p = FaFwdParams.from_buffer_copy(plan.params)
     p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
     p.sm_scale = sm_scale
@@ -449,7 +477,6 @@ def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
     else:
         with torch.cuda.device(dev):
             _launch_on(lib, p, plan, dev, q.device)
-    return out, lse
 
 
 def _launch_on(lib, p, plan, dev, device):

@@ -155,6 +155,37 @@ def test_unaligned_strides_are_copied(fa):
     assert (out.float() - o64.to(torch.float16).float()).abs().max().item() <= O_TOL[torch.float16]
 
 
+def test_repeated_calls_take_the_fast_path(fa, monkeypatch):
+    """A repeated call configuration skips the checks and reuses its launch plan; it must
+    give the same result, follow KV_SPLITS changes, and copy a misaligned view whose
+    shape and strides match a cached key."""
+    g = torch.Generator().manual_seed(21)
+    B, H, S, D = 1, 2, 300, 64
+    buf = torch.randn((3, B * H * S * D + 8), generator=g).to(torch.float16).cuda()
+    q, k, v = (buf[i, :B * H * S * D].view(B, H, S, D) for i in range(3))
+    o64, l64 = attention_fp64(q, k, v, True, 0.125)
+    fa._FAST_PLANS.clear()
+    first, lse1 = fa.attention(q, k, v, True, 0.125, return_lse=True)
+    assert len(fa._FAST_PLANS) == 1
+    again, lse2 = fa.attention(q, k, v, True, 0.125, return_lse=True)
+    assert torch.equal(first, again) and torch.equal(lse1, lse2)
+    assert (again.float() - o64.to(torch.float16).float()).abs().max().item() <= O_TOL[torch.float16]
+    monkeypatch.setenv("KV_SPLITS", "2")
+    split, lse3 = fa.attention(q, k, v, True, 0.125, return_lse=True)
+    assert len(fa._FAST_PLANS) == 2  # a new key: the split plan
+    assert (split.float() - o64.to(torch.float16).float()).abs().max().item() <= O_TOL[torch.float16]
+    assert (lse3.double() - l64).abs().max().item() <= LSE_TOL
+    monkeypatch.delenv("KV_SPLITS")
+    # Same shape and strides, base 2 bytes off 16-byte alignment: copied, still right.
+    qm = buf[0, 1:1 + B * H * S * D].view(B, H, S, D)
+    assert qm.data_ptr() % 16 != 0 and qm.stride() == q.stride()
+    om = fa.attention(qm, k, v, True, 0.125)
+    o64m, _ = attention_fp64(qm.contiguous(), k, v, True, 0.125)
+    assert (om.float() - o64m.to(torch.float16).float()).abs().max().item() <= O_TOL[torch.float16]
+    with pytest.raises(ValueError, match="finite"):
+        fa.attention(q, k, v, True, float("nan"))
+
+
 @pytest.mark.parametrize("scale", [-0.3, 0.0, 2.5])
 def test_unusual_scales(fa, scale):
     g = torch.Generator().manual_seed(9)
