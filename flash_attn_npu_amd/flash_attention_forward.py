@@ -388,7 +388,10 @@ class _LaunchPlan:
 
 # Launch plans keyed by (shapes, strides, dtypes, causal, resolved tiling, program
 # count, split override): a call only copies the block and sets its pointers and scale.
+# Both plan caches are emptied when they reach _MAX_CACHED_PLANS entries (a process that
+# sees that many configurations rebuilds them as it goes).
 _PLANS = {}
+_MAX_CACHED_PLANS = 4096
 
 
 def _launch_plan(lib, q, k, v, out, causal, bm, bn, programs, split_env):
@@ -413,6 +416,8 @@ def _launch_plan(lib, q, k, v, out, causal, bm, bn, programs, split_env):
     if splits > 1:
         nbytes = int(lib.fa_split_workspace_bytes(ctypes.byref(p), splits))
         _check(nbytes if nbytes < 0 else 0, "fa_split_workspace_bytes")
+    if len(_PLANS) >= _MAX_CACHED_PLANS:
+        _PLANS.clear()
     plan = _PLANS[key] = _LaunchPlan(p, splits, nbytes)
     return plan
 
@@ -459,6 +464,8 @@ def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
     plan = _launch_plan(lib, qr, kr, vr, out_r, causal, bm_r, bn_r, _get_persistent_programs(), _get_kv_splits())
     _launch(plan, qr, kr, vr, out_r, lse, sm_scale)
     if qr is q and kr is k and vr is v and out_r is out:
+        if len(_FAST_PLANS) >= _MAX_CACHED_PLANS:
+            _FAST_PLANS.clear()
         _FAST_PLANS[key] = plan
     return out_r, lse
 

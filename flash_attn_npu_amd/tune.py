@@ -60,7 +60,7 @@ import statistics
 import sys
 import tempfile
 import time
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 from pathlib import Path
 
 import torch
@@ -86,7 +86,6 @@ class Case:
     sm_scale: float
     seed: int
     workload: str | None = None   # name of a benchmark workload (inputs from workloads.make_inputs)
-    extra: dict = field(default_factory=dict)
 
     @property
     def key(self) -> str:
