@@ -64,6 +64,7 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
@@ -795,7 +796,9 @@ fa_fwd_dma_kernel(KernelArgs p) {
       const float m_cand = mx * c;
       const bool upd = m_cand > m_run + kLazyMaxThreshold;
       const float m_new = upd ? m_cand : m_run;
-      if (__builtin_amdgcn_ballot_w64(upd)) {
+      // Rows whose running max is still -inf have O = 0 and l = 0: nothing to rescale
+      // (every row in a unit's first tile).
+      if (__builtin_amdgcn_ballot_w64(upd && m_run != -INFINITY)) {
         const float alpha = upd ? fast_exp2(m_run - m_new) : 1.f;
         if constexpr (MSUM)
           lacc[0] *= alpha;
@@ -1312,7 +1315,9 @@ fa_fwd_pp_kernel(KernelArgs p) {
       const float m_cand = mx * c;
       const bool upd = m_cand > m_run + kLazyMaxThreshold;
       const float m_new = upd ? m_cand : m_run;
-      if (__builtin_amdgcn_ballot_w64(upd)) {
+      // Rows whose running max is still -inf have O = 0 and l = 0: nothing to rescale
+      // (every row in a unit's first tile).
+      if (__builtin_amdgcn_ballot_w64(upd && m_run != -INFINITY)) {
         const float alpha = upd ? fast_exp2(m_run - m_new) : 1.f;
         l_run *= alpha;
 #pragma unroll
@@ -1435,12 +1440,14 @@ fa_fwd_pp_kernel(KernelArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Split-KV merge.  One wave per (b, h, row): with m = max_s LSE_s and
-// w_s = exp(LSE_s - m),
+// Split-KV merge.  With m = max_s LSE_s and w_s = exp(LSE_s - m),
 //     LSE = m + ln(sum_s w_s),   O = sum_s w_s O_s / sum_s w_s,
 // exact for partial results normalised by their own row sums (O_s) with
 // natural-log LSE_s; runs with no visible key have LSE_s = -inf, w_s = 0.
 // HBM-bound: reads splits * (D + 1) fp32 per row, writes D halves + 1 fp32.
+// D / 4 lanes share a row, each loading 16 bytes of every O_s and storing
+// 8 bytes of O, so a wave moves whole 64-byte segments (256 / D rows per
+// wave, 1024 / D per block).
 struct MergeArgs {
   const float *part_o;   // [splits][B*H][Sq][D]
   const float *part_lse; // [splits][B*H][Sq]
@@ -1452,40 +1459,34 @@ struct MergeArgs {
 
 template <bool BF16>
 __global__ void __launch_bounds__(256) fa_merge_kernel(MergeArgs a) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lpr_log2 = 29 - __builtin_clz((unsigned)a.D);  // log2(D / 4): D is a power of two
+  const int li = threadIdx.x & ((1 << lpr_log2) - 1);       // this lane's 4 columns: 4 li .. 4 li + 3
   const int64_t rows = (int64_t)a.B * a.H * a.Sq;
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t row = ((int64_t)blockIdx.x << (8 - lpr_log2)) + (threadIdx.x >> lpr_log2);
   if (row >= rows) return;
   const int bh = (int)(row / a.Sq);
   const int q = (int)(row - (int64_t)bh * a.Sq);
   const int64_t plane = rows;  // rows per split
   float m = -INFINITY;
   for (int s = 0; s < a.splits; ++s) m = fmaxf(m, a.part_lse[s * plane + row]);
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   float wsum = 0.f;
+#pragma unroll 4
   for (int s = 0; s < a.splits; ++s) {
     const float ls = a.part_lse[s * plane + row];
     const float w = ls == -INFINITY ? 0.f : fast_exp2((ls - m) * kLog2e);
     wsum += w;
-    const float *src = a.part_o + (s * plane + row) * a.D;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = lane + 64 * i;
-      if (d < a.D) acc[i] += w * src[d];
-    }
+    const f32x4_t x = *(const f32x4_t *)(a.part_o + (s * plane + row) * a.D + 4 * li);
+    acc += w * x;
   }
   const float inv = 1.f / wsum;
   const int bb = bh / a.H, hh = bh - bb * a.H;
   char *dst = a.o + 2 * (bb * a.o_sb + hh * a.o_sh + (int64_t)q * a.o_ss);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int d = lane + 64 * i;
-    if (d < a.D) {
-      const uint32_t v = pack2<BF16>(acc[i] * inv, 0.f);
-      *(uint16_t *)(dst + 2 * d) = (uint16_t)(v & 0xffffu);
-    }
-  }
-  if (a.lse != nullptr && lane == 0) a.lse[row] = m + __logf(wsum);
+  u32x2_t v;
+  v[0] = pack2<BF16>(acc[0] * inv, acc[1] * inv);
+  v[1] = pack2<BF16>(acc[2] * inv, acc[3] * inv);
+  *(u32x2_t *)(dst + 8 * li) = v;
+  if (a.lse != nullptr && li == 0) a.lse[row] = m + __logf(wsum);
 }
 
 // ---------------------------------------------------------------------------
@@ -1677,7 +1678,8 @@ int launch(const fa_fwd_params *p, void *hip_stream, int splits, void *workspace
     m.o_sb = a.o_sb; m.o_sh = a.o_sh; m.o_ss = a.o_ss;
     m.B = p->B; m.H = p->H; m.Sq = p->Sq; m.D = p->D; m.splits = splits;
     const int64_t rows = (int64_t)p->B * p->H * p->Sq;
-    const unsigned blocks = (unsigned)((rows + 3) / 4);
+    const int64_t rows_per_block = 1024 / p->D;  // D / 4 lanes per row, 256 lanes
+    const unsigned blocks = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
     if (out_is_bf16(p->dtype)) {
       hipLaunchKernelGGL(fa_merge_kernel<true>, dim3(blocks), dim3(256), 0, stream, m);
     } else {

@@ -344,18 +344,24 @@ int32_t fa_default_kv_splits(const fa_fwd_params *p) {
   if (make_plan(p, &plan) != FA_OK) return 1;
   const KernelMeta &e = kKernelMeta[plan.kernel];
   if (!e.splittable) return 1;
-  // Split only a grid that would leave most workgroup slots empty, and only
-  // into runs of at least 8 KV tiles and 512 keys (the merge costs an extra
-  // HBM pass).
-  // Slots count at most two workgroups per CU: a third or fourth one only
-  // fills VALU issue gaps, and splitting further to occupy it cost more in
-  // merge work (B2 H4 S4096 D16 causal: 3 splits 8% slower than 2).
-  const int64_t slots = (int64_t)(e.wg_per_cu < 2 ? e.wg_per_cu : 2) * kDefaultCuCount;
-  if (plan.total_tiles * 2 > slots) return 1;
-  const int64_t kv_tiles = ((int64_t)p->Sk + plan.BN - 1) / plan.BN;
-  int64_t splits = (slots + plan.total_tiles - 1) / plan.total_tiles;
-  const int64_t min_run = 512 / plan.BN > 8 ? 512 / plan.BN : 8;  // KV tiles
-  if (splits > kv_tiles / min_run) splits = kv_tiles / min_run;
+  // Fitted to 25 shapes timed on MI355X with 1..8 splits (B1-2, H1-16,
+  // S256-16384, D16-256, fp16):
+  //  * only grids of at most half a workgroup per CU split: at one tile per
+  //    CU (256) a second workgroup per CU gained nothing (B1 H8 S4096 D64:
+  //    50 -> 54 us with 2 splits) or at most 3-5%;
+  //  * the runs fill one workgroup per CU, two for causal grids, whose
+  //    longest m-tile (all keys) sets the time while the others finish
+  //    early (B1 H4 S4096 D128 causal: 62 -> 42 us at 2, 41 at 4);
+  //  * each run keeps at least 64K key-columns (Sk / splits * D >= 65536):
+  //    below that the merge launch and its HBM pass cost more than the
+  //    shorter runs save (B1 H4 S1024 D64: 14.7 -> 15.7 us at 2 splits).
+  // These picks were within 8% of the fastest split count on every shape
+  // timed (18 of 25 the fastest), against up to 18% slower under the earlier
+  // rule (at least 8 KV tiles and 512 keys a run, up to two workgroups per CU).
+  if (plan.total_tiles * 2 > kDefaultCuCount) return 1;
+  const int64_t fill = (p->causal ? 2 : 1) * kDefaultCuCount / plan.total_tiles;
+  const int64_t work = (int64_t)p->Sk * p->D / 65536;
+  int64_t splits = fill < work ? fill : work;
   if (splits > kMaxKvSplits) splits = kMaxKvSplits;
   return splits > 1 ? (int32_t)splits : 1;
 }

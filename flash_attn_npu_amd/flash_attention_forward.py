@@ -37,8 +37,9 @@ RESULT_DIR_NAME = "result_dir"
 # way every workgroup walks its share of the balanced tile schedule (the
 # reference's persistent grid, flash_attention_forward.py:24,616-623).
 DEFAULT_PERSISTENT_PROGRAMS = 0
-# 0 = the library's split-KV choice (fa_default_kv_splits: only grids that
-# would leave most workgroup slots empty); KV_SPLITS in [1, 64] overrides.
+# 0 = the library's split-KV choice (fa_default_kv_splits: only grids of at
+# most half a tile per CU, into runs that stay long); KV_SPLITS in [1, 64]
+# overrides.
 DEFAULT_KV_SPLITS = 0
 # Name prefix of the attention kernels in a profiler trace (fa_fwd_dma_kernel,
 # fa_fwd_pp_kernel); the reference names its Triton kernel here

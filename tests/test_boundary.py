@@ -409,10 +409,19 @@ def test_split_workspace_bytes(lib):
     assert lib.fa_split_workspace_bytes(ctypes.byref(p), 65) == -9
 
 
-@pytest.mark.parametrize("shape,splits", [((1, 1, 4096, 128), 8), ((1, 8, 512, 64), 1), ((4, 32, 2048, 128), 1),
-                                          ((1, 1, 16384, 64), 4), ((1, 1, 300, 64), 1)])
-def test_default_kv_splits(lib, shape, splits):
-    p = _params(shape=shape, causal=0)
+@pytest.mark.parametrize("shape,causal,splits", [
+    ((1, 1, 4096, 128), 0, 8),    # 32 tiles: one run per CU, 512-key runs
+    ((1, 8, 512, 64), 0, 1),      # runs below 64K key-columns
+    ((1, 4, 1024, 64), 0, 1),
+    ((4, 32, 2048, 128), 0, 1),   # grid already fills the chip
+    ((1, 8, 4096, 64), 0, 1),     # 256 tiles: one per CU, no split
+    ((1, 1, 16384, 64), 0, 2),    # 128 tiles: two runs fill the CUs
+    ((1, 1, 16384, 64), 1, 4),    # causal: two runs per CU
+    ((1, 4, 2048, 128), 1, 4),
+    ((1, 2, 2048, 256), 1, 8),
+    ((1, 1, 300, 64), 0, 1)])
+def test_default_kv_splits(lib, shape, causal, splits):
+    p = _params(shape=shape, causal=causal)
     assert lib.fa_default_kv_splits(ctypes.byref(p)) == splits
 
 

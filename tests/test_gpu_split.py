@@ -73,9 +73,10 @@ def test_default_split_choice(fa):
 
 def test_small_grids_are_not_split(fa):
     """Config 1 (B1 H8 S512 D64, 32 tiles) and similar small grids stay unsplit: split
-    into 2, 4 or 8 runs they measured 13.4 -> 17.0-18.9 us back to back on MI355X (the
-    merge launch costs more than the shorter runs save).  The shape's preset (128-key
-    tiles) is the fastest by HIP-graph replay."""
+    into 2, 4 or 8 runs they measured 11.2 -> 15.1-15.5 us back to back on MI355X (the
+    merge launch costs more than the shorter runs save; the other four shapes: 11.1-14.8
+    -> 15.2-22.5 us).  The shape's preset (128-key tiles) is the fastest by HIP-graph
+    replay."""
     w = next(c for c in W.CONFIGS if c.name == "small-fp16")
     rt = fa._describe_runtime(w.B, w.H, w.S, w.D, w.causal, dtype=w.dtype)
     assert rt["kv_splits"] == 1 and rt["tiling_source"] == "preset"
