@@ -14,7 +14,22 @@ schema, one entry per pass:
                  "l2": {...}, "l2_columns": [...]}}
 
 so `python compare_results_plus.py A/profile_summary.json B/profile_summary.json`
-compares two MI355X runs unmodified.
+compares two MI355X runs unmodified.  The kernel-trace pass also traces the
+HIP API, which fills the entry's `step` and `api` sections:
+
+* step: one step per launch of the target kernel, from its start to the next
+  launch's start (the last ends with the last kernel).  Computing is the time
+  some kernel ran, Free the rest; there are no collectives, so the
+  communication, overlap and bubble columns are 0, Stage is the step's span
+  and Preparing is 0 (a step begins with its kernel).  Each column is the
+  median over steps, so the few long gaps between a benchmark's phases do not
+  stand for every step (the reference averages the 30 steps of one loop).
+* api: `launch` is the HIP launch call of each target dispatch (matched by
+  correlation id), `launch_all` every kernel launch call, and each HIP
+  *Synchronize function its own row; the reference's comparison tool prints
+  the device-wide synchronisation row under the Ascend runtime's name
+  (aclrtSynchronizeDeviceWithTimeout), which here holds hipDeviceSynchronize
+  (what torch.cuda.synchronize calls).
 
     python -m flash_attn_npu_amd.rocprof run --out result_dir -- python3 bench.py --steps 5 --cpu-seconds 0
     python -m flash_attn_npu_amd.rocprof summarize result_dir
@@ -33,7 +48,7 @@ from pathlib import Path
 
 PROFILE_OP_NAME = "fa_fwd"
 
-# One entry per rocprofv3 run.  None = kernel trace only.  Each counter list
+# One entry per rocprofv3 run.  None = kernel + HIP API trace.  Each counter list
 # fits one pass (<= 8 SQ, <= 4 TCC (FETCH_SIZE takes 3, WRITE_SIZE 2), <= 2 GRBM).
 METRIC_PLAN = {
     "KernelTrace": None,
@@ -139,8 +154,98 @@ def summarize_pass(pass_dir: Path, op: str = PROFILE_OP_NAME) -> dict:
         entry["l2"] = {"l2_count": 1.0, "Hit Rate": k["TCC_HIT_sum"] / tot if tot else None}
         entry["l2_columns"] = ["Hit Rate"]
     entry["kernel_columns"] = [c for c in k if c != "kernel_count"]
-    entry["api"] = {"launch": {"Count": entry["op"].get("Count")}}
+    entry["step"] = summarize_steps(pass_dir, op)
+    entry["api"] = summarize_api(pass_dir, op)
     return entry
+
+
+STEP_COLUMNS = ["Computing", "Communication(Not Overlapped)", "Overlapped", "Communication", "Free",
+                "Stage", "Bubble", "Communication(Not Overlapped and Exclude Receive)", "Preparing"]
+API_COLUMNS = ["Time(us)", "Count", "Avg(us)", "Min(us)", "Max(us)"]
+DEVICE_SYNC_KEY = "aclrtSynchronizeDeviceWithTimeout"  # the row name the comparison tool prints
+
+
+def _kernel_intervals(pass_dir: Path):
+    """(name, start_ns, end_ns, correlation id or None) of every dispatch in the pass."""
+    out = []
+    for tr in _find(pass_dir, "kernel_trace.csv"):
+        for r in _read_csv(tr):
+            corr = r.get("Correlation_Id")
+            out.append((r["Kernel_Name"], float(r["Start_Timestamp"]), float(r["End_Timestamp"]),
+                        int(float(corr)) if corr not in (None, "") else None))
+    out.sort(key=lambda x: x[1])
+    return out
+
+
+def summarize_steps(pass_dir: Path, op: str = PROFILE_OP_NAME) -> dict:
+    """Step Trace columns (us) from the kernel trace; see the module docstring."""
+    kernels = _kernel_intervals(Path(pass_dir))
+    starts = [s for name, s, _, _ in kernels if _is_target(name, op)]
+    if not starts:
+        return {}
+    last_end = max(e for _, _, e, _ in kernels)
+    bounds = starts + [last_end]
+    steps = []
+    j = 0  # first kernel that may overlap the current step
+    for lo, hi in zip(bounds[:-1], bounds[1:]):
+        while j < len(kernels) and kernels[j][2] <= lo:
+            j += 1
+        busy, cur_s, cur_e = 0.0, None, None
+        for _, s, e, _ in kernels[j:]:
+            if s >= hi:
+                break
+            s, e = max(s, lo), min(e, hi)
+            if e <= s:
+                continue
+            if cur_e is None or s > cur_e:
+                busy += (cur_e - cur_s) if cur_e is not None else 0.0
+                cur_s, cur_e = s, e
+            else:
+                cur_e = max(cur_e, e)
+        busy += (cur_e - cur_s) if cur_e is not None else 0.0
+        span = hi - lo
+        steps.append({"Computing": busy / 1e3, "Free": (span - busy) / 1e3, "Stage": span / 1e3})
+    out = {c: 0.0 for c in STEP_COLUMNS}
+    for c in ("Computing", "Free", "Stage"):
+        out[c] = statistics.median(st[c] for st in steps)
+    out["step_count"] = float(len(steps))
+    return out
+
+
+def _api_row(durations_us: list[float]) -> dict:
+    return {"Time(us)": sum(durations_us), "Count": float(len(durations_us)),
+            "Avg(us)": statistics.mean(durations_us), "Min(us)": min(durations_us),
+            "Max(us)": max(durations_us)}
+
+
+def summarize_api(pass_dir: Path, op: str = PROFILE_OP_NAME) -> dict:
+    """API Statistic rows from the HIP API trace; see the module docstring."""
+    pass_dir = Path(pass_dir)
+    calls: dict[str, list[tuple[int | None, float]]] = {}
+    for tr in _find(pass_dir, "hip_api_trace.csv"):
+        for r in _read_csv(tr):
+            name = r.get("Function") or r.get("Operation") or r.get("Name") or ""
+            corr = r.get("Correlation_Id")
+            dur = (float(r["End_Timestamp"]) - float(r["Start_Timestamp"])) / 1e3
+            calls.setdefault(name, []).append((int(float(corr)) if corr not in (None, "") else None, dur))
+    if not calls:
+        return {}
+    target_corr = {c for name, _, _, c in _kernel_intervals(pass_dir) if _is_target(name, op) and c is not None}
+    launch_all, launch_target = [], []
+    api = {}
+    for name, rows in sorted(calls.items()):
+        if "LaunchKernel" in name:
+            launch_all += [d for _, d in rows]
+            launch_target += [d for c, d in rows if c in target_corr]
+            api[name] = _api_row([d for _, d in rows])
+        elif "Synchronize" in name:
+            api[name] = _api_row([d for _, d in rows])
+    if launch_all:
+        api["launch_all"] = _api_row(launch_all)
+        api["launch"] = _api_row(launch_target) if launch_target else api["launch_all"]
+    if "hipDeviceSynchronize" in api:
+        api[DEVICE_SYNC_KEY] = dict(api["hipDeviceSynchronize"])
+    return api
 
 
 def _dispatch_key(row: dict, index: int):
@@ -215,6 +320,14 @@ def write_profile_summary_files(root: Path, summary_by_metric: dict):
         if s.get("kernel_columns"):
             lines.append("kernel_metrics: " + ", ".join(
                 f"{c}={_fmt(s['kernel'].get(c))}" for c in s["kernel_columns"]))
+        step, api = s.get("step", {}), s.get("api", {})
+        if step:
+            lines.append("step: computing_us={}, free_us={}, bubble_us={}, preparing_us={}".format(
+                _fmt(step.get("Computing")), _fmt(step.get("Free")), _fmt(step.get("Bubble")),
+                _fmt(step.get("Preparing"))))
+        if api:
+            lines.append("api: launch_avg_us={}, sync_avg_us={}".format(
+                _fmt(api.get("launch", {}).get("Avg(us)")), _fmt(api.get(DEVICE_SYNC_KEY, {}).get("Avg(us)"))))
         if s.get("l2_columns"):
             lines.append("l2_cache: " + ", ".join(f"{c}={_fmt(s['l2'].get(c), 6)}" for c in s["l2_columns"]))
         lines.append("")
@@ -248,7 +361,8 @@ def run_passes(out: Path, target: list[str], plan=None, timeout=120) -> dict:
     for name, counters in plan.items():
         pdir = out / name
         cmd = ["rocprofv3"]
-        cmd += ["--kernel-trace", "--stats"] if counters is None else ["--pmc", *counters]
+        # Traces (kernel + HIP API) and counters never share a run.
+        cmd += ["--kernel-trace", "--hip-trace", "--stats"] if counters is None else ["--pmc", *counters]
         cmd += ["-d", str(pdir), "-o", "run", "--output-format", "csv", "--", *target]
         print(f"[rocprof] pass {name}: {' '.join(cmd)}", flush=True)
         proc = subprocess.run(cmd, env=env, cwd="/tmp", timeout=timeout, capture_output=True, text=True)

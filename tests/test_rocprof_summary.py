@@ -99,3 +99,74 @@ def test_summary_files_carry_the_comparison_tool_keys(passes):
         assert key in op
     text = t.read_text()
     assert "[KernelTrace]" in text and "avg_us=152.000" in text and "Hit Rate=0.740000" in text
+
+
+def test_step_trace_from_kernel_trace(passes):
+    """Steps run from one attention launch to the next; the copy at 600 us falls in
+    the last step, which ends with it (650 us)."""
+    step = rocprof.summarize_pass(passes / "KernelTrace")["step"]
+    # Steps: [0, 200) busy 150; [200, 400) busy 152; [400, 650) busy 154 + 50.
+    assert step["Computing"] == pytest.approx(152.0)           # median of 150, 152, 204
+    assert step["Free"] == pytest.approx(48.0)                 # median of 50, 48, 46
+    assert step["Stage"] == pytest.approx(200.0)               # median of 200, 200, 250
+    assert step["step_count"] == 3.0
+    for col in ("Communication", "Overlapped", "Bubble", "Preparing"):
+        assert step[col] == 0.0
+    assert set(rocprof.STEP_COLUMNS) <= set(step)
+
+
+def test_step_trace_merges_overlapping_kernels(tmp_path):
+    d = tmp_path / "KernelTrace"
+    d.mkdir()
+    # Two target launches 100 us apart; an overlapping 30 us kernel inside the first
+    # step (40..70 against 0..50) and an idle gap: busy = 70, not 80.
+    _write_trace(d / "run_kernel_trace.csv", [(KERNEL, 0, 50_000), (COPY, 40_000, 30_000), (KERNEL, 100_000, 10_000)])
+    step = rocprof.summarize_steps(d)
+    assert step["step_count"] == 2.0
+    assert step["Computing"] == pytest.approx((70.0 + 10.0) / 2)
+    assert step["Stage"] == pytest.approx((100.0 + 10.0) / 2)
+
+
+def _write_rows(path, fields, rows):
+    with path.open("w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=fields)
+        w.writeheader()
+        for r in rows:
+            w.writerow(dict(zip(fields, r)))
+
+
+def test_api_statistic_from_hip_trace(tmp_path):
+    d = tmp_path / "KernelTrace"
+    d.mkdir()
+    _write_rows(d / "run_kernel_trace.csv", ["Kernel_Name", "Correlation_Id", "Start_Timestamp", "End_Timestamp"],
+                [(KERNEL, 7, 1_000, 2_000), (COPY, 8, 3_000, 4_000), (KERNEL, 9, 5_000, 6_000)])
+    _write_rows(d / "run_hip_api_trace.csv", ["Domain", "Function", "Correlation_Id", "Start_Timestamp", "End_Timestamp"],
+                [("HIP_RUNTIME_API", "hipLaunchKernel", 7, 0, 4_000),
+                 ("HIP_RUNTIME_API", "hipLaunchKernel", 8, 0, 9_000),
+                 ("HIP_RUNTIME_API", "hipLaunchKernel", 9, 0, 6_000),
+                 ("HIP_RUNTIME_API", "hipDeviceSynchronize", 10, 0, 20_000),
+                 ("HIP_RUNTIME_API", "hipDeviceSynchronize", 11, 0, 40_000),
+                 ("HIP_RUNTIME_API", "hipEventSynchronize", 12, 0, 5_000),
+                 ("HIP_RUNTIME_API", "hipMalloc", 13, 0, 100_000)])
+    api = rocprof.summarize_api(d)
+    # launch = the attention kernel's own launch calls (correlation 7 and 9): 4 and 6 us.
+    assert api["launch"] == {"Time(us)": 10.0, "Count": 2.0, "Avg(us)": 5.0, "Min(us)": 4.0, "Max(us)": 6.0}
+    assert api["launch_all"]["Count"] == 3.0 and api["launch_all"]["Max(us)"] == 9.0
+    sync = api[rocprof.DEVICE_SYNC_KEY]
+    assert sync == api["hipDeviceSynchronize"] and sync["Avg(us)"] == 30.0 and sync["Count"] == 2.0
+    assert api["hipEventSynchronize"]["Count"] == 1.0
+    assert "hipMalloc" not in api
+    for row in api.values():
+        assert set(row) == set(rocprof.API_COLUMNS)
+
+
+def test_summary_text_carries_step_and_api_lines(tmp_path, passes):
+    d = passes / "KernelTrace" / "host"
+    _write_rows(d / "run_hip_api_trace.csv", ["Function", "Correlation_Id", "Start_Timestamp", "End_Timestamp"],
+                [("hipLaunchKernel", 1, 0, 3_000), ("hipDeviceSynchronize", 2, 0, 8_000)])
+    summary = rocprof.summarize_dir(passes, plan={"KernelTrace": None})
+    _, t = rocprof.write_profile_summary_files(tmp_path / "out", summary)
+    text = t.read_text()
+    # The trace has no correlation ids: launch falls back to every launch call.
+    assert "step: computing_us=152.000, free_us=48.000, bubble_us=0.000, preparing_us=0.000" in text
+    assert "api: launch_avg_us=3.000, sync_avg_us=8.000" in text
