@@ -797,8 +797,11 @@ fa_fwd_dma_kernel(KernelArgs p) {
       const bool upd = m_cand > m_run + kLazyMaxThreshold;
       const float m_new = upd ? m_cand : m_run;
       // Rows whose running max is still -inf have O = 0 and l = 0: nothing to rescale
-      // (every row in a unit's first tile).
-      if (__builtin_amdgcn_ballot_w64(upd && m_run != -INFINITY)) {
+      // (every row in a unit's first tile).  Not in the D = 128 kernels at three
+      // workgroups per CU, whose 168-register budget the extra compare overflows
+      // (an 8-register spill).
+      constexpr bool kSkipFirstRescale = !(D >= 128 && OCC >= 3);
+      if (__builtin_amdgcn_ballot_w64(upd && (!kSkipFirstRescale || m_run != -INFINITY))) {
         const float alpha = upd ? fast_exp2(m_run - m_new) : 1.f;
         if constexpr (MSUM)
           lacc[0] *= alpha;

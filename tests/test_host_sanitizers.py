@@ -9,18 +9,23 @@
 * The kernel source is compiled for gfx950 from scratch with the library's own
   recipe (hipcc cross-compiles without a GPU), and the fresh library must
   describe the same kernel table and carry the same source hash as the one in
-  the tree, so the boundary tests never pass on a stale build.
+  the tree, so the boundary tests never pass on a stale build.  The same
+  compile reports each kernel's registers (-Rpass-analysis=kernel-resource-usage):
+  every kernel must reach the occupancy its table entry launches with, and no
+  kernel that the default tiling or a preset selects may use scratch.
 """
 
 from __future__ import annotations
 
 import ctypes
 import os
+import re
 import shutil
 import subprocess
 from pathlib import Path
 
 import pytest
+import torch
 
 from flash_attn_npu_amd import build as B
 from flash_attn_npu_amd import flash_attention_forward as fa
@@ -60,7 +65,8 @@ def _table(lib):
                     reason="needs hipcc")
 def test_kernel_source_compiles_for_gfx950_and_matches_the_tree(tmp_path):
     out = tmp_path / "libfa_fresh.so"
-    proc = subprocess.run(B.compile_command(out), capture_output=True, text=True, timeout=900)
+    cmd = B.compile_command(out, extra=["-Rpass-analysis=kernel-resource-usage"])
+    proc = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     assert proc.returncode == 0, proc.stderr[-4000:]
     fresh = ctypes.CDLL(str(out))
     fresh.fa_build_id.restype = ctypes.c_char_p
@@ -69,3 +75,81 @@ def test_kernel_source_compiles_for_gfx950_and_matches_the_tree(tmp_path):
         "the library in the tree was not built from the current sources"
     assert _table(fresh) == _table(tree)
     assert fresh.fa_params_size() == tree.fa_params_size() == ctypes.sizeof(fa.FaFwdParams)
+    _check_resources(_resource_remarks(proc.stderr), _table(tree))
+
+
+def _resource_remarks(stderr):
+    """{mangled kernel name: {remark key: int value}} from the compiler's report."""
+    kernels, cur = {}, None
+    for line in stderr.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            cur = kernels.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"remark:\s+([A-Za-z][A-Za-z /\[\]]*?): (\d+) \[-Rpass-analysis", line)
+        if m and cur is not None:
+            cur[m.group(1).strip()] = int(m.group(2))
+    return kernels
+
+
+_DMA = re.compile(r"fa_fwd_dma_kernelILi(\d+)ELi(\d+)ELi(\d+)ELi\d+ELi(\d+)ELb([01])ELb([01])ELb([01])E")
+_PP = re.compile(r"fa_fwd_pp_kernelILi(\d+)ELi(\d+)ELi\d+ELb([01])ELb([01])E")
+
+
+def _entry_key(row):
+    """The template arguments that name table entry `row` = (D, dtype, causal, BM, BN, waves, wg/CU)."""
+    d, dtype, causal, _, bn, nw, wg = row
+    bf16, v8 = int(dtype in (1, 3)), int(dtype in (2, 3))
+    if nw == 8:
+        return ("pp", d, bn, bf16, causal)
+    return ("dma", d, bn, nw, wg, bf16, causal, v8)
+
+
+def _remark_key(name):
+    m = _DMA.search(name)
+    if m:
+        d, bn, nw, occ, bf16, causal, v8 = map(int, m.groups())
+        return ("dma", d, bn, nw, occ, bf16, causal, v8)
+    m = _PP.search(name)
+    if m:
+        d, bn, bf16, causal = map(int, m.groups())
+        return ("pp", d, bn, bf16, causal)
+    return None
+
+
+def _default_kernel_ids():
+    """Kernels the library's default tiling or a preset selects, over head dims, dtypes,
+    fp8 V, masks and lengths."""
+    ids = set()
+    for d in (16, 32, 64, 128, 256):
+        for dt in (torch.float16, torch.bfloat16):
+            for v8 in (None, fa.FP8_V_DTYPE):
+                for causal in (False, True):
+                    for n in (64, 512, 2048, 8192):
+                        ids.add(fa._describe_runtime(2, 4, n, d, causal, dtype=dt, v_dtype=v8)["kernel_id"])
+    for dt in (torch.float16, torch.bfloat16):
+        for (z, h, n, d, causal) in fa._presets_for(dt):
+            ids.add(fa._describe_runtime(z, h, n, d, causal, dtype=dt)["kernel_id"])
+    return ids
+
+
+def _check_resources(remarks, table):
+    by_key = {}
+    for name, res in remarks.items():
+        key = _remark_key(name)
+        if key is not None:
+            assert key not in by_key, f"two kernels named {key}"
+            by_key[key] = (name, res)
+    for i, row in enumerate(table):
+        name, res = by_key[_entry_key(row)]
+        waves_per_simd = row[6] * row[5] // 4
+        assert res["Occupancy [waves/SIMD]"] >= waves_per_simd, \
+            f"entry {i} ({name}) reaches {res['Occupancy [waves/SIMD]']} waves/SIMD, launched with {waves_per_simd}"
+    defaults = _default_kernel_ids()
+    assert len(defaults) >= 10
+    for i in sorted(defaults):
+        name, res = by_key[_entry_key(table[i])]
+        assert res["ScratchSize [bytes/lane]"] == 0 and res["VGPRs Spill"] == 0, \
+            f"default kernel {i} ({name}) spills: {res}"
+    merge = [res for name, res in remarks.items() if "fa_merge_kernel" in name]
+    assert len(merge) == 2 and all(r["ScratchSize [bytes/lane]"] == 0 for r in merge)
