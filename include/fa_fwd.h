@@ -179,8 +179,9 @@ int fa_fwd_split(const fa_fwd_params *p, int32_t kv_splits, void *workspace, int
                  void *hip_stream);
 
 /* The library's split choice for these parameters: > 1 only when the
- * unsplit grid would fill less than half of the resident workgroup slots and
- * each run keeps at least 8 KV tiles.  Host-only. */
+ * unsplit grid has at most one (head, m-tile) tile per two CUs; the runs then
+ * fill one workgroup per CU (two for a causal mask), each keeping at least
+ * 65536 key-columns (Sk / splits * D).  Host-only. */
 int32_t fa_default_kv_splits(const fa_fwd_params *p);
 
 /* ---- No-allocation split-KV.  No counterpart in the reference.  For callers
