@@ -99,3 +99,65 @@ def test_random_cases_vs_fp64(fa, monkeypatch, chunk):
         d_lse = (lse.double() - l64).abs().max().item()
         assert d_lse <= LSE_TOL, (i, d_lse)
     monkeypatch.delenv("KV_SPLITS", raising=False)
+
+
+# ---------------------------------------------------------------------------
+# fp8-e5m2 V: the same kind of draw (no tiling override: the fp8-V kernels have
+# one tiling each), checked per head with the gates of tests/test_gpu_fp8v.py
+# (the CPU replay of the kernel's e5m2 rounding, the fp32 formula's e5m2
+# bound, LSE); with forced splits only the e5m2 bound and LSE apply, since
+# each KV run rounds p against its own running max.
+
+N_FP8 = 48
+
+
+def _draw_fp8(i):
+    rng = random.Random(SEED + 7919 + i)
+    d = rng.choice([16, 32, 64, 128, 128, 256])
+    return dict(d=d, dtype=rng.choice([torch.float16, torch.bfloat16]), causal=rng.random() < 0.5,
+                s=rng.randint(1, 130) if rng.random() < 0.4 else rng.randint(131, 900),
+                b=rng.randint(1, 2), h=rng.randint(1, 2),
+                scale=d ** -0.5 * rng.choice([0.5, 1.0, 2.0]) * (-1.0 if rng.random() < 0.15 else 1.0),
+                layouts=[rng.choice(["bhsd", "bshd", "pitch"]) for _ in range(3)],
+                splits=rng.choice([None, None, None, 2, 5]), seed=SEED + 7919 + i)
+
+
+@pytest.mark.parametrize("chunk", range(N_FP8 // 12))
+def test_random_fp8v_cases(fa, monkeypatch, chunk):
+    import numpy as np
+    from oracle.attention_oracle import attention_ref
+    from tests.test_gpu_fp8v import _check_head, _probs
+
+    for i in range(chunk * 12, (chunk + 1) * 12):
+        c = _draw_fp8(i)
+        print(f"[random-fp8v] case {i}: " + ", ".join(f"{k}={v}" for k, v in c.items()), flush=True)
+        g = torch.Generator().manual_seed(c["seed"])
+        shape = (c["b"], c["h"], c["s"], c["d"])
+        q = _tensor(shape, c["layouts"][0], c["dtype"], 1.0, g, 8)
+        k = _tensor(shape, c["layouts"][1], c["dtype"], 1.0, g, 16)
+        v = _tensor(shape, c["layouts"][2], torch.float8_e5m2, 1.0, g, 16)  # fp8 rows: 16-element pitch
+        if c["splits"] is None:
+            monkeypatch.delenv("KV_SPLITS", raising=False)
+            # The library's own split choice applies to fp8 V as well (e.g. B1 H2 S560 D256).
+            splits = fa._describe_runtime(*shape, c["causal"], dtype=c["dtype"],
+                                          v_dtype=torch.float8_e5m2)["kv_splits"]
+        else:
+            monkeypatch.setenv("KV_SPLITS", str(c["splits"]))
+            splits = c["splits"]
+        out, lse = fa.attention(q, k, v, c["causal"], c["scale"], return_lse=True)
+        assert torch.isfinite(out).all() and torch.isfinite(lse).all(), i
+        out, lse = out.float().cpu().numpy(), lse.cpu().numpy()
+        for bi in range(c["b"]):
+            for hi in range(c["h"]):
+                qh, kh, vh = (t[bi, hi].float().cpu().numpy() for t in (q, k, v))
+                if splits == 1:
+                    _check_head(qh, kh, vh, out[bi, hi], lse[bi, hi], c["causal"], c["scale"], c["dtype"],
+                                schedule_check=False)
+                else:
+                    dt = "float16" if c["dtype"] == torch.float16 else "bfloat16"
+                    ref, rl = attention_ref(qh, kh, vh, c["causal"], c["scale"], out_dtype=dt)
+                    p = _probs(qh, kh, c["causal"], c["scale"])
+                    bound = 2.0 ** -2 * (p @ np.abs(vh).astype(np.float64)) + O_TOL[c["dtype"]]
+                    assert np.all(np.abs(out[bi, hi] - ref) <= bound), i
+                    assert np.abs(lse[bi, hi] - rl).max() <= LSE_TOL, i
+    monkeypatch.delenv("KV_SPLITS", raising=False)
