@@ -1,8 +1,8 @@
 """CPU oracle for the FlashAttention forward path.
 
 TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg may import this module, and only as the checker (or the timed
-CPU baseline).  The product path (flash_attn_npu_amd) never calls it: on a
+cpu_baseline leg may import this module, and only as the reference that results
+are compared against (or the timed CPU baseline).  The product path (flash_attn_npu_amd) never calls it: on a
 machine without the HIP library the product raises instead of falling back.
 
 What it restates

@@ -1,6 +1,6 @@
 """Device-side float64 attention, used as the full-size reference in GPU tests.
 
-The CPU oracle (oracle/attention_oracle.py) is the primary checker; at the
+The CPU oracle (oracle/attention_oracle.py) is the primary reference; at the
 full sizes of the measured configurations it runs on sampled heads only, and
 this float64 restatement of the same formula (evaluate_attention.py:134-143)
 covers every head on the GPU.  Float64 keeps it clear of any reduced-precision
