@@ -379,12 +379,13 @@ class _LaunchPlan:
     the parameter block (shape, strides, dtype, mask, tiling, program count), the
     split count and its workspace size.  Built once per configuration."""
 
-    __slots__ = ("params", "splits", "workspace_bytes")
+    __slots__ = ("params", "splits", "workspace_bytes", "lse_shape")
 
-    def __init__(self, params, splits, workspace_bytes):
+    def __init__(self, params, splits, workspace_bytes, lse_shape):
         self.params = params
         self.splits = splits
         self.workspace_bytes = workspace_bytes
+        self.lse_shape = lse_shape
 
 
 # Launch plans keyed by (shapes, strides, dtypes, causal, resolved tiling, program
@@ -419,7 +420,7 @@ def _launch_plan(lib, q, k, v, out, causal, bm, bn, programs, split_env):
         _check(nbytes if nbytes < 0 else 0, "fa_split_workspace_bytes")
     if len(_PLANS) >= _MAX_CACHED_PLANS:
         _PLANS.clear()
-    plan = _PLANS[key] = _LaunchPlan(p, splits, nbytes)
+    plan = _PLANS[key] = _LaunchPlan(p, splits, nbytes, (z, h, n_ctx))
     return plan
 
 
@@ -431,10 +432,25 @@ def _launch_plan(lib, q, k, v, out, causal, bm, bn, programs, split_env):
 _FAST_PLANS = {}
 
 
-def _call_key(q, k, v, causal, bm, bn):
+# The two variables are read on every call.  On POSIX os.environ keeps its entries in a
+# plain dict of bytes (shared with os.environb and updated by every change made through
+# either): a lookup there costs ~0.1 us, against ~1.5 us through os.environ.get, which
+# encodes the key and decodes the value on every access.
+_ENV_BYTES = getattr(os.environ, "_data", None) if os.name == "posix" else None
+if not isinstance(_ENV_BYTES, dict):
+    _ENV_BYTES = None
+
+
+def _env_key():
+    if _ENV_BYTES is not None:
+        return _ENV_BYTES.get(b"PERSISTENT_PROGRAMS"), _ENV_BYTES.get(b"KV_SPLITS")
     env = os.environ
+    return env.get("PERSISTENT_PROGRAMS"), env.get("KV_SPLITS")
+
+
+def _call_key(q, k, v, causal, bm, bn):
     return (q.shape, k.shape, v.shape, q.stride(), k.stride(), v.stride(), q.dtype, k.dtype, v.dtype,
-            q.device, k.device, v.device, causal, bm, bn, env.get("PERSISTENT_PROGRAMS"), env.get("KV_SPLITS"))
+            q.get_device(), k.get_device(), v.get_device(), causal, bm, bn, _env_key())
 
 
 def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
@@ -447,7 +463,7 @@ def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):
     plan = _FAST_PLANS.get(key)
     if plan is not None and not (q.data_ptr() | k.data_ptr() | v.data_ptr()) & 15:
         out = torch.empty_like(q)
-        lse = torch.empty(q.shape[:3], device=q.device, dtype=torch.float32)
+        lse = q.new_empty(plan.lse_shape, dtype=torch.float32)
         _launch(plan, q, k, v, out, lse, sm_scale)
         return out, lse
     _validate_inputs(q, k, v)
@@ -479,32 +495,41 @@ def _launch(plan, q, k, v, out, lse, sm_scale):
     p = FaFwdParams.from_buffer_copy(plan.params)
     p.q, p.k, p.v, p.o, p.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
     p.sm_scale = sm_scale
-    dev = q.device.index
-    if dev == torch.cuda.current_device():
-        _launch_on(lib, p, plan, dev, q.device)
+    dev = q.get_device()
+    if dev == _current_device():
+        _launch_on(lib, p, plan, dev, q)
     else:
         with torch.cuda.device(dev):
-            _launch_on(lib, p, plan, dev, q.device)
+            _launch_on(lib, p, plan, dev, q)
 
 
-def _launch_on(lib, p, plan, dev, device):
-    """Launch on the current stream of device `dev` (the current device)."""
+def _launch_on(lib, p, plan, dev, q):
+    """Launch on the current stream of device `dev` (the current device, q's)."""
     stream = _current_raw_stream(dev)
     pp = ctypes.byref(p)
     if plan.splits > 1:
-        workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=device)  # 512 B aligned
+        workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=q.device)  # 512 B aligned
         _check(lib.fa_fwd_split(pp, plan.splits, workspace.data_ptr(), plan.workspace_bytes, stream),
                "fa_fwd_split")
     else:
         _check(lib.fa_fwd(pp, stream), "fa_fwd")
 
 
+# torch's own accessors for the current device and raw stream, resolved once (the
+# public torch.cuda.current_device / current_stream(dev).cuda_stream are the fallback).
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_GET_DEVICE = getattr(torch._C, "_cuda_getDevice", None)
+
+
 def _current_raw_stream(dev):
     """hipStream_t of torch's current stream on device `dev`, as an int."""
-    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
-    if raw is not None:
-        return raw(dev)
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(dev)
     return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _current_device():
+    return _GET_DEVICE() if _GET_DEVICE is not None else torch.cuda.current_device()
 
 
 def attention(q, k, v, causal, sm_scale, BM=None, BN=None, return_lse=False):

@@ -301,6 +301,28 @@ def test_fallback_tiling_cached_per_shape(monkeypatch):
     assert fa.get_tiling(*key) == (128, 32)
 
 
+def test_call_key_follows_the_environment(monkeypatch):
+    """The repeated-call cache key reads PERSISTENT_PROGRAMS and KV_SPLITS on every call
+    (through os.environ's own dict on POSIX): a change made through os.environ gives a
+    new key, and undoing it gives the old one back."""
+    q = torch.zeros((1, 2, 40, 64), dtype=torch.float16)
+    monkeypatch.delenv("KV_SPLITS", raising=False)
+    monkeypatch.delenv("PERSISTENT_PROGRAMS", raising=False)
+    base = fa._call_key(q, q, q, True, None, None)
+    monkeypatch.setenv("KV_SPLITS", "3")
+    split = fa._call_key(q, q, q, True, None, None)
+    monkeypatch.setenv("PERSISTENT_PROGRAMS", "7")
+    both = fa._call_key(q, q, q, True, None, None)
+    assert len({base, split, both}) == 3
+    monkeypatch.setenv("KV_SPLITS", "4")
+    assert fa._call_key(q, q, q, True, None, None) != both
+    monkeypatch.delenv("KV_SPLITS")
+    monkeypatch.delenv("PERSISTENT_PROGRAMS")
+    assert fa._call_key(q, q, q, True, None, None) == base
+    assert fa._call_key(q, q, q, False, None, None) != base
+    assert fa._call_key(q.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3), q, q, True, None, None) != base
+
+
 def test_kernel_ready_fast_path_and_copies():
     t = torch.zeros((2, 3, 40, 64), dtype=torch.float16)
     assert fa._kernel_ready(t) is t  # contiguous, 16-byte aligned: read in place
