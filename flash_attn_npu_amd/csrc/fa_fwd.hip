@@ -75,6 +75,13 @@ constexpr float kLn2 = 0.6931471805599453f;
 // The running max only moves when a row max exceeds it by more than this many
 // log2 units, so un-normalised probabilities stay <= 2^8 (safe in fp16/bf16).
 constexpr float kLazyMaxThreshold = 8.0f;
+// Tiles after a unit's first keep the running max while every lane's sum of
+// p over the tile (which bounds each of its p) stays within a bound: 2^14
+// when P is rounded to fp16 or e5m2 (a quarter of their largest finite
+// values), 2^32 for bf16 P (fp32's exponent range; l and O stay far from
+// overflow).
+template <bool BF16_P>
+constexpr float kLazyMaxSum = BF16_P ? 4294967296.0f : 16384.0f;
 // FA_TIMING (development builds only): the ping-pong kernel accumulates, per
 // wave, the shader-clock cycles spent in each phase and writes them to
 // KernelArgs::timing.  The product build compiles none of it.
@@ -452,6 +459,12 @@ fa_fwd_dma_kernel(KernelArgs p) {
   // faster at D = 16; at D = 32 equal and at D = 64 1.3-1.8% slower, where
   // the extra MFMA time costs what the adds saved.
   constexpr bool MSUM = !BF16 && !V8 && D == 16;
+  // Tiles after a unit's first take the row max only when p outgrows 2^8
+  // (see the tile body); the kept scores then cost D * BN / 64 more live
+  // registers, which the kernels with 128-key tiles, 64-key D = 256 tiles or
+  // the 168-register budget of three D = 128 workgroups per CU cannot spare
+  // (they spill): those take the row max of every tile.
+  constexpr bool kSumTrigger = !MSUM && BN <= 64 && D * BN <= 8192 && !(D >= 128 && OCC >= 3);
   constexpr int BM = C::BM;
   // One array per stage: the compiler's LDS-DMA alias tracking then knows
   // that DMAs into one stage never feed reads of the other, and adds no
@@ -655,9 +668,12 @@ fa_fwd_dma_kernel(KernelArgs p) {
     // the mask (and for skipping tiles above a wave's own rows), and neither
     // loop body branches on it.  STG = t % 2 is compile-time too, so every
     // LDS read address is a per-lane base plus an immediate offset.
-    auto kv_tile = [&](int t, auto masked_tag, auto stage_tag) __attribute__((always_inline)) {
+    auto kv_tile = [&](int t, auto masked_tag, auto stage_tag, auto exact_tag) __attribute__((always_inline)) {
       constexpr bool MASKED = decltype(masked_tag)::value;
       constexpr int STG = decltype(stage_tag)::value;
+      constexpr bool EXACT = decltype(exact_tag)::value;  // the unit's first tile
+      // Tiles after the first of 64 keys (16-bit V) take the block-split body.
+      constexpr bool SPLIT = kSumTrigger && !EXACT && !V8 && BN == 64;
 #ifdef FA_TIMING
       const uint32_t ta = FA_CLK();
       if (t == 0) tm_pro = ta - tm0;
@@ -739,6 +755,144 @@ fa_fwd_dma_kernel(KernelArgs p) {
       f32x16_t sacc[BN / 32];
 #pragma unroll
       for (int kb = 0; kb < BN / 32; ++kb) sacc[kb] = (f32x16_t){};
+      // p = 2^(s c - mb) per 32-key block.
+      f32x16_t pacc[BN / 32];
+      auto rescale = [&](float alpha) __attribute__((always_inline)) {
+        if constexpr (MSUM)
+          lacc[0] *= alpha;
+        else
+          l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < C::DB; ++db) oacc[db] *= alpha;
+      };
+      // Register r of block kb holds key kbase + 4h + (32kb + 8(r>>2) + (r&3));
+      // it is visible iff that offset <= lim.
+      auto mask_block = [&](int kb) __attribute__((always_inline)) {
+        const int last_key = CAUSAL ? min(qrow, p.Sk - 1) : p.Sk - 1;
+        const int lim = last_key - kbase - 4 * h;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int off = 32 * kb + 8 * (r >> 2) + (r & 3);
+          sacc[kb][r] = off <= lim ? sacc[kb][r] : -INFINITY;
+        }
+      };
+
+      if constexpr (SPLIT) {
+        // Two 32-key blocks, each carried through on its own: the QK MFMAs
+        // run block by block, block 0's exponentials issue between block 1's
+        // QK MFMAs, and block 1's between block 0's P.V MFMAs, so the wave
+        // keeps the matrix core busy through most of its own softmax.  The
+        // running max is handled per block as in the whole-tile form (it
+        // moves only when a block's lane sum exceeds kLazyMaxSum; O and l,
+        // including block 0's P.V, are then rescaled): exact by shift
+        // invariance.
+        constexpr int NS = D / 16;  // k-steps per block
+        auto kread_b = [&](int i) {
+          const int kb = i / NS, s = i % NS;
+          return *(const u32x4_t *)(sbase + kro[s] + 32 * kb * C::ROW);
+        };
+        float bpart[2];
+        auto exps_block = [&](int kb, float m) __attribute__((always_inline)) {
+          const float mb = (m == -INFINITY) ? 0.f : m;
+          float lsum[4];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float pv = fast_exp2(__builtin_fmaf(sacc[kb][r], c, -mb));
+            pacc[kb][r] = pv;
+            lsum[r & 3] = r < 4 ? pv : lsum[r & 3] + pv;
+          }
+          bpart[kb] = (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+        };
+        auto settle_block = [&](int kb) __attribute__((always_inline)) {
+          if (__builtin_amdgcn_ballot_w64(!(bpart[kb] <= kLazyMaxSum<BF16 && !V8>))) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+            const float m_new = fmaxf(m_run, halves_max(mx) * c);
+            rescale(m_new == m_run ? 1.f : fast_exp2(m_run - m_new));
+            m_run = m_new;
+            exps_block(kb, m_run);
+          }
+          l_run += bpart[kb];
+        };
+        u32x4_t pf[4];
+        auto pack_block = [&](int kb) __attribute__((always_inline)) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+              pf[2 * kb + u][w] = pack2<BF16>(pacc[kb][8 * u + 2 * w], pacc[kb][8 * u + 2 * w + 1]);
+        };
+        // Number of softmax VALU instructions placed after each MFMA.
+        constexpr int kValuPerMfma = 7;
+        constexpr int kSchedValu = 0x002 | 0x400;  // VALU and TRANS
+
+        // S^T = K Q^T block by block (reads KPF ahead, one DMA per MFMA),
+        // block 0's softmax under block 1's MFMAs.
+#pragma unroll
+        for (int i = 0; i < KPF; ++i) kfr[i] = kread_b(i);
+#pragma unroll
+        for (int i = 0; i < NQK; ++i) {
+          if (i + KPF < NQK) kfr[i + KPF] = kread_b(i + KPF);
+          if (i + KPF == NQK) {
+#pragma unroll
+            for (int j = 0; j < VPF; ++j) vfr[j] = vread(j);
+          }
+          const int kb = i / NS, s = i % NS;
+          sacc[kb] = mfma32x32x16<BF16>(kfr[i], qf[s], sacc[kb]);
+          if (i < NDMA) dma(NEXT{}, rk_n, rv_n, i);
+        }
+        if (MASKED) mask_block(0);
+        exps_block(0, m_run);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, KPF, 0);
+#pragma unroll
+        for (int i = 0; i < NQK; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          if (i < NDMA) __builtin_amdgcn_sched_group_barrier(kSchedVmem, 1, 0);
+          if (i + KPF < NQK) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+          if (i + KPF == NQK) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, VRD * VPF, 0);
+          if (i >= NS) __builtin_amdgcn_sched_group_barrier(kSchedValu, kValuPerMfma, 0);
+        }
+        settle_block(0);
+
+        // O^T += V^T P^T for block 0's keys (k-steps 0, 1) with block 1's
+        // softmax between the MFMAs, then block 1's keys.
+        if constexpr (D >= 128) __builtin_amdgcn_s_setprio(1);
+        pack_block(0);
+        constexpr int NPVB = 2 * C::DB;  // P.V MFMAs per block
+#pragma unroll
+        for (int i = 0; i < NPVB; ++i) {
+          vfr[i + VPF] = vread(i + VPF);
+          const int ks = i / C::DB, db = i % C::DB;
+          oacc[db] = mfma32x32x16<BF16>(vfr[i], pf[ks], oacc[db]);
+        }
+        if (MASKED) mask_block(1);
+        exps_block(1, m_run);
+        __builtin_amdgcn_sched_group_barrier(kSchedValu, 8, 0);  // block 0's packs
+#pragma unroll
+        for (int i = 0; i < NPVB; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedValu, kValuPerMfma, 0);
+        }
+        settle_block(1);
+        pack_block(1);
+#pragma unroll
+        for (int i = NPVB; i < NPV; ++i) {
+          if (i + VPF < NPV) vfr[i + VPF] = vread(i + VPF);
+          const int ks = i / C::DB, db = i % C::DB;
+          oacc[db] = mfma32x32x16<BF16>(vfr[i], pf[ks], oacc[db]);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSchedValu, 8, 0);
+#pragma unroll
+        for (int i = NPVB; i < NPV - VPF; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, VPF, 0);
+        if constexpr (D >= 128) __builtin_amdgcn_s_setprio(0);
+        return;
+      }
       // Written in issue order (read i + KPF, MFMA i, DMA i), which also
       // bounds the fragments' live ranges if the schedule below is relaxed.
       auto kread = [&](int i) {
@@ -774,54 +928,70 @@ fa_fwd_dma_kernel(KernelArgs p) {
       }
 
       if (MASKED) {
-        // Register r of block kb holds key kbase + 4h + (32kb + 8(r>>2) + (r&3));
-        // it is visible iff that offset <= lim.
-        const int last_key = CAUSAL ? min(qrow, p.Sk - 1) : p.Sk - 1;
-        const int lim = last_key - kbase - 4 * h;
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb) mask_block(kb);
+      }
+
+      // Row max of the tile in log2 units (both lane halves of a row).
+      auto tile_max = [&]() __attribute__((always_inline)) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < BN / 32; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+        return halves_max(mx) * c;
+      };
+      // p = 2^(s c - mb) into pacc, and this lane's sum of them (half a row).
+      float part = 0.f;
+      auto exps = [&](float m) __attribute__((always_inline)) {
+        const float mb = (m == -INFINITY) ? 0.f : m;
+        float lsum[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kb = 0; kb < BN / 32; ++kb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int off = 32 * kb + 8 * (r >> 2) + (r & 3);
-            sacc[kb][r] = off <= lim ? sacc[kb][r] : -INFINITY;
+            const float pv = fast_exp2(__builtin_fmaf(sacc[kb][r], c, -mb));
+            pacc[kb][r] = pv;
+            lsum[r & 3] = (kb == 0 && r < 4) ? pv : lsum[r & 3] + pv;
           }
-      }
-
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < BN / 32; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
-      mx = halves_max(mx);
-      const float m_cand = mx * c;
-      const bool upd = m_cand > m_run + kLazyMaxThreshold;
-      const float m_new = upd ? m_cand : m_run;
-      // Rows whose running max is still -inf have O = 0 and l = 0: nothing to rescale
-      // (every row in a unit's first tile).  Not in the D = 128 kernels at three
-      // workgroups per CU, whose 168-register budget the extra compare overflows
-      // (an 8-register spill).
-      constexpr bool kSkipFirstRescale = !(D >= 128 && OCC >= 3);
-      if (__builtin_amdgcn_ballot_w64(upd && (!kSkipFirstRescale || m_run != -INFINITY))) {
-        const float alpha = upd ? fast_exp2(m_run - m_new) : 1.f;
-        if constexpr (MSUM)
-          lacc[0] *= alpha;
-        else
-          l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < C::DB; ++db) oacc[db] *= alpha;
-      }
-      m_run = m_new;
-      const float mb = (m_new == -INFINITY) ? 0.f : m_new;
-
-      float lsum[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb = 0; kb < BN / 32; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pv = fast_exp2(__builtin_fmaf(sacc[kb][r], c, -mb));
-          sacc[kb][r] = pv;
-          lsum[r & 3] = (kb == 0 && r < 4) ? pv : lsum[r & 3] + pv;
+        part = (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+      };
+      if constexpr (kSumTrigger && EXACT) {
+        // A unit's first tile: every running max is still -inf and O = 0,
+        // l = 0, so the tile's row max becomes the running max (rows with no
+        // visible key keep -inf and get p = 0).
+        m_run = tile_max();
+        exps(m_run);
+      } else if constexpr (kSumTrigger) {
+        // Later tiles use the running max as it stands, so the row max costs
+        // nothing on most tiles.  It moves only when a lane's sum of p over
+        // the tile exceeds kLazyMaxSum (which bounds each p).  Then (rare: a
+        // logit beyond any seen before by 14 or 32 log2 units) the tile's row max becomes
+        // the running max, O and l are rescaled and p is recomputed from the
+        // scores, which are kept.  Exact by shift invariance; NaN or inf
+        // sums also take the exact path.
+        exps(m_run);
+        if (__builtin_amdgcn_ballot_w64(!(part <= kLazyMaxSum<BF16 && !V8>))) {
+          const float m_new = fmaxf(m_run, tile_max());
+          rescale(m_new == m_run ? 1.f : fast_exp2(m_run - m_new));
+          m_run = m_new;
+          exps(m_run);
         }
+      } else {
+        // The row max of every tile, moved lazily (by more than 2^8 only).
+        // Rows whose running max is still -inf hold O = 0 and l = 0: nothing
+        // to rescale (every row in a unit's first tile), except in the D = 128
+        // kernels at three workgroups per CU, whose 168-register budget the
+        // extra compare overflows (a spill); alpha = 0 keeps such rows at 0.
+        constexpr bool kSkipFirstRescale = !(D >= 128 && OCC >= 3);
+        const float m_cand = tile_max();
+        const bool upd = m_cand > m_run + kLazyMaxThreshold;
+        const float m_new = upd ? m_cand : m_run;
+        if (__builtin_amdgcn_ballot_w64(upd && (!kSkipFirstRescale || m_run != -INFINITY)))
+          rescale(upd ? fast_exp2(m_run - m_new) : 1.f);
+        m_run = m_new;
+        exps(m_run);
+      }
 
       if constexpr (V8) {
         // P^T in e5m2 (round to nearest even), per 64-key chunk kc: byte j =
@@ -832,10 +1002,10 @@ fa_fwd_dma_kernel(KernelArgs p) {
 #pragma unroll
           for (int w = 0; w < 8; ++w) {
             const int kb = 2 * kc + (w >> 2), r0 = 4 * (w & 3);
-            const int lo = __builtin_amdgcn_cvt_pk_bf8_f32(sacc[kb][r0], sacc[kb][r0 + 1], 0, false);
-            pf8[kc][w] = __builtin_amdgcn_cvt_pk_bf8_f32(sacc[kb][r0 + 2], sacc[kb][r0 + 3], lo, true);
+            const int lo = __builtin_amdgcn_cvt_pk_bf8_f32(pacc[kb][r0], pacc[kb][r0 + 1], 0, false);
+            pf8[kc][w] = __builtin_amdgcn_cvt_pk_bf8_f32(pacc[kb][r0 + 2], pacc[kb][r0 + 3], lo, true);
           }
-        l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+        l_run += part;
         // O^T += V^T P^T: one fp8 MFMA per (64 keys, 32 head dims) (unit
         // scales: E8M0 exponent 127 = 2^0), the next fragment's four reads
         // ahead of it.
@@ -858,9 +1028,9 @@ fa_fwd_dma_kernel(KernelArgs p) {
       for (int ks = 0; ks < BN / 16; ++ks) {
         const int kb = ks >> 1, t8 = (ks & 1) * 8;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) pf[ks][w] = pack2<BF16>(sacc[kb][t8 + 2 * w], sacc[kb][t8 + 2 * w + 1]);
+        for (int w = 0; w < 4; ++w) pf[ks][w] = pack2<BF16>(pacc[kb][t8 + 2 * w], pacc[kb][t8 + 2 * w + 1]);
       }
-      if constexpr (!MSUM) l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+      if constexpr (!MSUM) l_run += part;
 
       // O^T += V^T P^T; the A operand is two transpose reads (keys +0..3 and
       // +8..11 of the k-step), VPF fragments ahead of their MFMA.  For
@@ -895,14 +1065,24 @@ fa_fwd_dma_kernel(KernelArgs p) {
     const int n_full = n_full_of(q0);
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
+    using NotFirst = std::integral_constant<bool, false>;
     int t = t_begin;
     auto run = [&](int end, auto masked_tag) __attribute__((always_inline)) {
-      if (t < end && (t & 1)) kv_tile(t++, masked_tag, S1{});
+      if (t < end && (t & 1)) kv_tile(t++, masked_tag, S1{}, NotFirst{});
       for (; t + 1 < end; t += 2) {
-        kv_tile(t, masked_tag, S0{});
-        kv_tile(t + 1, masked_tag, S1{});
+        kv_tile(t, masked_tag, S0{}, NotFirst{});
+        kv_tile(t + 1, masked_tag, S1{}, NotFirst{});
       }
-      if (t < end) kv_tile(t++, masked_tag, S0{});
+      if (t < end) kv_tile(t++, masked_tag, S0{}, NotFirst{});
+    };
+    // The unit's first tile (it sets the running max), in its stage.
+    auto first_tile = [&](auto masked_tag) __attribute__((always_inline)) {
+      using First = std::integral_constant<bool, true>;
+      if (t & 1)
+        kv_tile(t, masked_tag, S1{}, First{});
+      else
+        kv_tile(t, masked_tag, S0{}, First{});
+      ++t;
     };
     // Tiles [t, end) in which this wave has nothing to compute: only keep the
     // DMA ring and the barriers in step with the other waves (one barrier
@@ -938,9 +1118,17 @@ fa_fwd_dma_kernel(KernelArgs p) {
     if (OCC >= 2 && q0w >= p.Sq) {
       idle_tiles(n_tiles);
     } else {
-      run(n_full, std::integral_constant<bool, false>{});
+      using Unmasked = std::integral_constant<bool, false>;
+      using Masked = std::integral_constant<bool, true>;
       const int n_act = (CAUSAL && OCC >= 2) ? max(n_full, min(n_tiles, wave_last_q / BN + 1)) : n_tiles;
-      run(n_act, std::integral_constant<bool, true>{});
+      if constexpr (kSumTrigger) {
+        if (t < n_full)
+          first_tile(Unmasked{});
+        else if (t < n_act)
+          first_tile(Masked{});
+      }
+      run(n_full, Unmasked{});
+      run(n_act, Masked{});
       idle_tiles(n_tiles);
     }
 #ifdef FA_TIMING

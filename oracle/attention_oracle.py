@@ -41,17 +41,25 @@ unnormalised probabilities of each KV tile, p = exp(s - m) against the running
 row max m, are cast to e5m2 (`p.to(tl.float8e5)`) before `tl.dot(p, v)`,
 while the row sum l accumulates the unrounded fp32 p.  Where the cast falls
 depends on the tile size and on when m moves, so the function replays one
-schedule, given by `block_n` and `lazy_threshold`: tiles of block_n keys from
-key 0, exp2 of (s * c - m) with c = |sm_scale| * log2(e) in fp32, and m moved
-only when a tile's max exceeds it by more than lazy_threshold (in log2 units;
-0 is the reference's always-move rule).  `round_e5m2` is the OCP e5m2 format
+schedule, given by `block_n` and `schedule`: tiles of block_n keys from key 0,
+exp2 of (s * c - m) with c = |sm_scale| * log2(e) in fp32, and m moved
+ * schedule="max": only when a tile's max exceeds it by more than
+   lazy_threshold (in log2 units; 0 is the reference's always-move rule);
+ * schedule="sum": to the first tile's exact row max, then only for the
+   32-row groups (one wavefront's rows) in which some row's sum of p over
+   the keys of one half of the tile (keys whose offset in the tile has bit 2
+   equal to 0, or to 1) exceeds sum_bound; every row of such a group then
+   takes max(m, tile max), O and l are rescaled and p is recomputed.
+`round_e5m2` is the OCP e5m2 format
 (1 sign, 5 exponent bits with bias 15, 2 mantissa bits, subnormals in steps
 of 2^-16, no saturation) with round-to-nearest-even.  Pinning: round_e5m2
 against known values from the format definition and against torch's
 float8_e5m2 cast; attention_fp8v with the cast disabled against
-attention_ref (online softmax = softmax, any block_n / threshold); with the
-cast, against attention_ref within the e5m2 error bound
-|O - O_ref| <= 2^-3 * sum_j (p_j / l) |v_j|, and an unchanged LSE.
+attention_ref (online softmax = softmax, any block_n / threshold / bound,
+including logit jumps that move m under either schedule); with the cast,
+against attention_ref within the e5m2 error bound
+|O - O_ref| <= 2^-3 * sum_j (p_j / l) |v_j|, and an unchanged LSE; the sum
+schedule's move against a never-move mutant (p past e5m2's range).
 
 Rounding helpers produce the fp16 / bf16 values the GPU path writes, so that
 an output can be compared to the oracle after the same final cast the
@@ -136,17 +144,27 @@ def round_e5m2(x: np.ndarray) -> np.ndarray:
 
 
 def attention_fp8v(q, k, v8, causal: bool, sm_scale: float, out_dtype: str | None = None,
-                   block_n: int = 64, lazy_threshold: float = 8.0, round_p: bool = True):
+                   block_n: int = 64, lazy_threshold: float = 8.0, round_p: bool = True,
+                   schedule: str = "max", sum_bound: float = 16384.0, group_rows: int = 32):
     """fp8-e5m2 V attention, replaying a tiled online-softmax schedule.
 
     q, k: [..., S, D] float32 values of the fp16/bf16 inputs; v8: [..., Sk, D]
-    float32 values of the e5m2 V.  For each tile of block_n keys (from key 0):
-    m_cand = fp32(max(s) * c); the row max moves to m_cand only when
-    m_cand > m + lazy_threshold (O and l are then rescaled by 2^(m - m_new));
-    p = 2^(s * c - m) in fp32 (m taken as 0 while no key was seen);
-    l += sum(p); O += e5m2(p) @ v  (round_p=False skips the cast).
+    float32 values of the e5m2 V.  For each tile of block_n keys (from key 0),
+    with m_cand = fp32(max(s) * c) and p = 2^(s * c - m) in fp32 (m taken as
+    0 while no key was seen):
+      schedule="max": the row max moves to m_cand only when
+        m_cand > m + lazy_threshold (O and l are then rescaled by 2^(m - m_new));
+      schedule="sum": tile 0 sets m = m_cand; on later tiles p is formed with
+        m as it stands, and in every group of group_rows rows where some row's
+        sum of p over either half of the tile's keys (offset bit 2 clear / set)
+        is not <= sum_bound, each row takes m_new = max(m, m_cand), O and l
+        are rescaled by 2^(m - m_new) (1 where m is unchanged) and p is
+        recomputed;
+    then l += sum(p); O += e5m2(p) @ v  (round_p=False skips the cast).
     Returns (out rounded to out_dtype, lse) like attention_ref.
     """
+    if schedule not in ("max", "sum"):
+        raise ValueError(f"unknown schedule {schedule!r}")
     q = np.asarray(q, dtype=np.float32)
     k = np.asarray(k, dtype=np.float32)
     v8 = np.asarray(v8, dtype=np.float32)
@@ -158,6 +176,13 @@ def attention_fp8v(q, k, v8, causal: bool, sm_scale: float, out_dtype: str | Non
     vf = v8.reshape(-1, sk, v8.shape[-1]).astype(np.float64)
     c = np.float32(np.float32(abs(sm_scale)) * np.float32(LOG2E))
     thr = np.float32(lazy_threshold)
+    bound = np.float32(sum_bound)
+    group = np.arange(sq) // group_rows
+
+    def exps(st, m):
+        mb = np.where(m == -np.inf, np.float32(0.0), m)
+        x = (st.astype(np.float64) * np.float64(c) - mb[:, None].astype(np.float64)).astype(np.float32)
+        return np.exp2(x).astype(np.float32)
     out = np.empty((qf.shape[0], sq, vf.shape[-1]), dtype=np.float32)
     lse = np.empty((qf.shape[0], sq), dtype=np.float32)
     rows = np.arange(sq)[:, None]
@@ -173,16 +198,34 @@ def attention_fp8v(q, k, v8, causal: bool, sm_scale: float, out_dtype: str | Non
             if causal:
                 st = np.where(np.arange(lo, hi)[None, :] > rows, np.float32(-np.inf), st)
             m_cand = (st.max(axis=1) * c).astype(np.float32)
-            upd = m_cand > (m + thr)
-            m_new = np.where(upd, m_cand, m)
-            with np.errstate(invalid="ignore"):
-                alpha = np.where(upd, np.exp2((m - m_new).astype(np.float32)), np.float32(1.0)).astype(np.float32)
-            l = (l * alpha).astype(np.float32)
-            acc *= alpha[:, None].astype(np.float64)
-            m = m_new
-            mb = np.where(m == -np.inf, np.float32(0.0), m)
-            x = (st.astype(np.float64) * np.float64(c) - mb[:, None].astype(np.float64)).astype(np.float32)
-            p = np.exp2(x).astype(np.float32)
+            if schedule == "sum" and lo == 0:
+                m = m_cand
+                p = exps(st, m)
+            elif schedule == "sum":
+                p = exps(st, m)
+                half = ((np.arange(hi - lo) >> 2) & 1).astype(bool)
+                with np.errstate(invalid="ignore"):
+                    over = ~(p[:, ~half].sum(axis=1, dtype=np.float32) <= bound)
+                    over |= ~(p[:, half].sum(axis=1, dtype=np.float32) <= bound)
+                moved = np.isin(group, np.unique(group[over]))
+                if moved.any():
+                    m_new = np.where(moved, np.maximum(m, m_cand), m).astype(np.float32)
+                    with np.errstate(invalid="ignore"):
+                        alpha = np.where(m_new == m, np.float32(1.0),
+                                         np.exp2((m - m_new).astype(np.float32))).astype(np.float32)
+                    l = (l * alpha).astype(np.float32)
+                    acc *= alpha[:, None].astype(np.float64)
+                    m = m_new
+                    p = exps(st, m)
+            else:
+                upd = m_cand > (m + thr)
+                m_new = np.where(upd, m_cand, m)
+                with np.errstate(invalid="ignore"):
+                    alpha = np.where(upd, np.exp2((m - m_new).astype(np.float32)), np.float32(1.0)).astype(np.float32)
+                l = (l * alpha).astype(np.float32)
+                acc *= alpha[:, None].astype(np.float64)
+                m = m_new
+                p = exps(st, m)
             l = (l + p.sum(axis=1, dtype=np.float32)).astype(np.float32)
             pr = round_e5m2(p) if round_p else p
             acc += pr.astype(np.float64) @ vf[i, lo:hi]

@@ -5,8 +5,10 @@ With V in float8_e5m2 the kernel, like the reference, rounds the unnormalised
 probabilities of each KV tile to e5m2 before P.V (and sums the unrounded ones
 into l).  Where that rounding lands depends on the tiling and on when the
 running max moves, so the oracle replays the kernel's schedule
-(`attention_fp8v`: 64-key tiles, 128 at D = 16, max moved only past a 2^8
-margin).  Gates:
+(`attention_fp8v`: 64-key tiles, 128 at D = 16; at D = 32, 64 and 128 the
+first tile's row max, moved for a wavefront's 32 rows only when a lane's sum
+of p over a tile passes 2^14; at D = 16 and 256 the max moved only past a
+2^8 margin).  Gates:
 
 * LSE: max|dLSE| <= 1e-3 against both the replay and the fp32 formula (l uses
   unrounded p, so the fp8 cast does not touch it).
@@ -57,8 +59,10 @@ def _check_head(qh, kh, vh, og, lg, causal, scale, dtype, schedule_check=True):
     """Gates for one (b, h); returns (max|dO| vs replay, rows over tol, max|dLSE|)."""
     dt = DT_ORACLE[dtype]
     tol = O_TOL[dtype]
-    bn = 128 if qh.shape[-1] == 16 else 64  # the fp8-V kernels' key tile
-    r8, rl8 = attention_fp8v(qh, kh, vh, causal, scale, out_dtype=dt, block_n=bn)
+    d = qh.shape[-1]
+    bn = 128 if d == 16 else 64  # the fp8-V kernels' key tile
+    schedule = "sum" if d in (32, 64, 128) else "max"  # the kernels' running-max rule
+    r8, rl8 = attention_fp8v(qh, kh, vh, causal, scale, out_dtype=dt, block_n=bn, schedule=schedule)
     ref, rl = attention_ref(qh, kh, vh, causal, scale, out_dtype=dt)
     p = _probs(qh, kh, causal, scale)
     av = np.abs(vh).astype(np.float64)

@@ -396,6 +396,53 @@ def test_fp8v_replay_without_cast_is_attention(causal, block_n, thr):
     assert np.abs(o - o_ref).max() < 2e-6 and np.abs(l - l_ref).max() < 2e-6
 
 
+def _jump_inputs(rs, shape, row, key, jump):
+    # q row `row` and k row `key` aligned so their logit exceeds every earlier
+    # one by about `jump` log2 units at sm_scale 0.125.
+    q, k, v = _qkv(rs, shape)
+    d = shape[-1]
+    u = np.ones(d, dtype=np.float32) / np.sqrt(d)
+    q[..., row, :] = u * 8.0
+    k[..., key, :] = u * np.float32(jump / (8.0 * 0.125 * 1.4426950408889634))
+    return q, k, v
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("bound", [16384.0, 1.0, 1e-3])
+def test_fp8v_sum_schedule_without_cast_is_attention(causal, bound):
+    # The sum schedule (first tile's max, moves per 32-row group past a lane
+    # sum bound) is an online softmax too: without the cast it is softmax,
+    # also when a logit jump (row 40, key 150) moves the max and when the
+    # bound forces moves on most tiles.
+    rs = np.random.RandomState(14)
+    q, k, v = _jump_inputs(rs, (2, 200, 64), 40, 150, 30.0)
+    o, l = attention_fp8v(q, k, v, causal, 0.125, round_p=False, schedule="sum", sum_bound=bound)
+    o_ref, l_ref = attention_ref(q, k, v, causal, 0.125)
+    # A few fp32 ulps (row 40's LSE is ~21).
+    assert np.abs(o - o_ref).max() < 2e-6
+    assert np.all(np.abs(l - l_ref) <= 1e-6 * (1.0 + np.abs(l_ref)))
+
+
+def test_fp8v_sum_schedule_moves_per_group():
+    # A logit 30 log2 units past row 40's first-tile max (key 150) gives
+    # p ~ 2^30, past e5m2's range: the sum schedule moves m for row 40's
+    # group (rows 32..63) and stays within the e5m2 bound of attention; a
+    # schedule that never moves (bound = inf) overflows there.  Rows of other
+    # groups keep their max and match the never-move replay bit for bit.
+    rs = np.random.RandomState(15)
+    q, k, v = _jump_inputs(rs, (1, 200, 64), 40, 150, 30.0)
+    o, l = attention_fp8v(q, k, v, False, 0.125, schedule="sum")
+    o_ref, l_ref = attention_ref(q, k, v, False, 0.125)
+    bound = 2.0 ** -3 * (_probs(q, k, False, 0.125) @ np.abs(v).astype(np.float64)) + 1e-6
+    assert np.all(np.abs(o - o_ref) <= bound)
+    assert np.all(np.abs(l - l_ref) <= 1e-6 * (1.0 + np.abs(l_ref)))
+    with np.errstate(all="ignore"):
+        o_never, _ = attention_fp8v(q, k, v, False, 0.125, schedule="sum", sum_bound=np.inf)
+    assert not np.isfinite(o_never[0, 40]).all()
+    others = np.r_[0:32, 64:200]
+    assert np.array_equal(o[0, others], o_never[0, others])
+
+
 def _probs(q, k, causal, scale):
     s = (q.astype(np.float64) @ k.astype(np.float64).swapaxes(-1, -2)) * scale
     if causal:
@@ -405,14 +452,15 @@ def _probs(q, k, causal, scale):
     return e / e.sum(axis=-1, keepdims=True)
 
 
+@pytest.mark.parametrize("schedule", ["max", "sum"])
 @pytest.mark.parametrize("causal", [False, True])
-def test_fp8v_within_e5m2_bound_of_attention(causal):
+def test_fp8v_within_e5m2_bound_of_attention(causal, schedule):
     # Rounding each p to nearest e5m2 moves it by at most 2^-3 p, so
     # |O - O_ref| <= 2^-3 sum_j (p_j / l) |v_j| elementwise; l (and LSE) use
     # the unrounded p.
     rs = np.random.RandomState(5)
     q, k, v = _qkv(rs, (2, 150, 64))
-    o, l = attention_fp8v(q, k, v, causal, 0.3)
+    o, l = attention_fp8v(q, k, v, causal, 0.3, schedule=schedule)
     o_ref, l_ref = attention_ref(q, k, v, causal, 0.3)
     bound = 2.0 ** -3 * (_probs(q, k, causal, 0.3) @ np.abs(v).astype(np.float64)) + 1e-6
     assert np.all(np.abs(o - o_ref) <= bound)
