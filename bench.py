@@ -42,16 +42,26 @@ def profile_summary_path(workload_tag: str) -> Path:
     return REPO / "profiles" / f"fa_fwd_{workload_tag}_rocprof.txt"
 
 
-def read_traffic(workload_tag: str):
-    """HBM bytes per launch from the committed rocprofv3 summary, if present.
+def read_traffic(workload_tag: str, build_id: str):
+    """HBM bytes per launch from the committed rocprofv3 summary, if it was made
+    with the library being benched.
 
     The summary (written by flash_attn_npu_amd.rocprof from FETCH_SIZE and
     WRITE_SIZE passes, each scaled by what the same counter reads for a plain
     256 MiB device copy in the same process) carries hbm_read_bytes= and
-    hbm_write_bytes= in its kernel_metrics lines.
+    hbm_write_bytes= in its kernel_metrics lines, and the profiled library's
+    fa_build_id in its build: line.  A summary of another build (or one with no
+    stamp) gives None: its bytes need not be this kernel's.
     """
+    from flash_attn_npu_amd.rocprof import read_build_id
+
     path = profile_summary_path(workload_tag)
     if not path.exists():
+        log(f"traffic: no summary {path.name}")
+        return None
+    stamped = read_build_id(path)
+    if stamped != build_id:
+        log(f"traffic: {path.name} was profiled with build {stamped}, this library is {build_id}: not used")
         return None
     vals = {}
     for line in path.read_text().splitlines():
@@ -126,6 +136,8 @@ def main(argv=None):
     ap.add_argument("--warmup-seconds", type=float, default=1.0)
     ap.add_argument("--config", type=int, default=2, help="1-based index of the measured configuration")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--block-m", type=int, default=None, help="BLOCK_M override (default: the library's tiling)")
+    ap.add_argument("--block-n", type=int, default=None, help="BLOCK_N override (default: the library's tiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after timing, run a plain 256 MiB device copy (rocprofv3 FETCH/WRITE calibration)")
     args = ap.parse_args(argv)
@@ -148,11 +160,11 @@ def main(argv=None):
     log(f"workload: {w.describe()} sm_scale={w.sm_scale:.6f}")
     q, k, v = make_inputs(w, device="cuda")
     torch.cuda.synchronize()
-    rt = fa._describe_runtime(w.B, w.H, w.S, w.D, w.causal, dtype=w.dtype)
+    rt = fa._describe_runtime(w.B, w.H, w.S, w.D, w.causal, bm=args.block_m, bn=args.block_n, dtype=w.dtype)
     log(f"runtime: {rt}")
 
     def step():
-        return fa.attention(q, k, v, w.causal, w.sm_scale, return_lse=w.with_lse)
+        return fa.attention(q, k, v, w.causal, w.sm_scale, BM=args.block_m, BN=args.block_n, return_lse=w.with_lse)
 
     # Warm up for at least W steps and at least one second, so the timed steps
     # run at the clocks a sustained load settles at.
@@ -217,7 +229,8 @@ def main(argv=None):
         del a, b
 
     tag = w.name
-    traffic = read_traffic(tag)
+    build_id = fa._load_library().fa_build_id().decode()
+    traffic = read_traffic(tag, build_id)
     result = {
         "metric": METRIC,
         "value": round(value, 2),

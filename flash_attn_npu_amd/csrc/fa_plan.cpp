@@ -270,11 +270,12 @@ int fa_validate(const fa_fwd_params *p) {
     if (rows[t] > 1 && st[t][2] < p->D) return FA_ERR_STRIDE;
     // Buffer offsets inside one (b, h) slice are 32-bit: keep the slice, plus
     // the rows past its end that a last partial m-tile or the DMAs issued past
-    // the last KV tile address, below 2 GiB.  (A seq stride this large is
-    // rejected before the product could overflow.)
+    // the last KV tile address, below 2 GiB.  rows < 2^31 and row_stride <
+    // 2^31 here, so the product is formed in 128-bit arithmetic (it can
+    // exceed int64: e.g. 2^31 rows of a 2^31 - 8 element stride).
     const int64_t row_stride = st[t][2] > p->D ? st[t][2] : p->D;
     if (row_stride >= ((int64_t)1 << 31)) return FA_ERR_SHAPE;
-    if ((rows[t] + kRowMargin) * row_stride * 2 >= ((int64_t)1 << 31)) return FA_ERR_SHAPE;
+    if ((__int128)(rows[t] + kRowMargin) * row_stride * 2 >= ((__int128)1 << 31)) return FA_ERR_SHAPE;
   }
   if ((int64_t)p->Sq * 4 >= ((int64_t)1 << 31)) return FA_ERR_SHAPE;
   if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o)) return FA_ERR_ALIGN;

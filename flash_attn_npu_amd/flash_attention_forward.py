@@ -77,6 +77,59 @@ DEFAULT_TILING_PRESETS_BF16 = {
 }
 # END AUTO-TUNED DEFAULT TILING PRESETS
 
+
+class _PresetTable(dict):
+    """A preset table that counts its changes, so the cached launch plans (which hold
+    the resolved tiling) follow a table edited in a live process the way the
+    reference, which reads its presets on every call, does.  Replacing a table
+    by another object is seen through its identity; a plain dict put in its
+    place is only followed when it is replaced again."""
+
+    version = 0
+
+    def _changed(self):
+        _PresetTable.version += 1
+
+    def __setitem__(self, key, value):
+        super().__setitem__(key, value)
+        self._changed()
+
+    def __delitem__(self, key):
+        super().__delitem__(key)
+        self._changed()
+
+    def update(self, *args, **kwargs):
+        super().update(*args, **kwargs)
+        self._changed()
+
+    def pop(self, *args):
+        out = super().pop(*args)
+        self._changed()
+        return out
+
+    def popitem(self):
+        out = super().popitem()
+        self._changed()
+        return out
+
+    def setdefault(self, key, default=None):
+        out = super().setdefault(key, default)
+        self._changed()
+        return out
+
+    def clear(self):
+        super().clear()
+        self._changed()
+
+    def __ior__(self, other):
+        out = super().__ior__(other)
+        self._changed()
+        return out
+
+
+DEFAULT_TILING_PRESETS = _PresetTable(DEFAULT_TILING_PRESETS)
+DEFAULT_TILING_PRESETS_BF16 = _PresetTable(DEFAULT_TILING_PRESETS_BF16)
+
 # --------------------------------------------------------------------------
 # C ABI binding (include/fa_fwd.h)
 
@@ -426,7 +479,8 @@ def _launch_plan(lib, q, k, v, out, causal, bm, bn, programs, split_env):
 
 # Calls whose q, k, v the kernel reads in place, keyed by everything the argument checks,
 # the tiling and the launch plan depend on (shapes, strides, dtypes, devices, mask,
-# BM/BN override, the two environment variables): a repeated call goes straight to
+# BM/BN override, the two environment variables, the preset tables' identity and change
+# count): a repeated call goes straight to
 # allocation and launch.  Tensors at a base address that is not 16-byte aligned take
 # the full path (and are copied there).
 _FAST_PLANS = {}
@@ -450,7 +504,8 @@ def _env_key():
 
 def _call_key(q, k, v, causal, bm, bn):
     return (q.shape, k.shape, v.shape, q.stride(), k.stride(), v.stride(), q.dtype, k.dtype, v.dtype,
-            q.get_device(), k.get_device(), v.get_device(), causal, bm, bn, _env_key())
+            q.get_device(), k.get_device(), v.get_device(), causal, bm, bn, _env_key(),
+            _PresetTable.version, id(DEFAULT_TILING_PRESETS), id(DEFAULT_TILING_PRESETS_BF16))
 
 
 def _launch_kernel(q, k, v, causal, sm_scale, bm=None, bn=None):

@@ -130,6 +130,8 @@ def summarize_pass(pass_dir: Path, op: str = PROFILE_OP_NAME) -> dict:
     k = entry["kernel"]
     for name, vals in counters.items():
         k[name] = statistics.mean(vals)
+        # A counter pass has no durations: count the dispatches sampled.
+        k.setdefault("kernel_count", float(len(vals)))
     # Derived figures.
     if "SQ_VALU_MFMA_BUSY_CYCLES" in k and "GRBM_GUI_ACTIVE" in k and k["GRBM_GUI_ACTIVE"]:
         # GRBM_GUI_ACTIVE sums the 8 XCDs' busy cycles.
@@ -302,14 +304,46 @@ def copy_factors(pass_dir: Path) -> dict:
     return {k: statistics.mean(v) for k, v in out.items()}
 
 
-def write_profile_summary_files(root: Path, summary_by_metric: dict):
-    """profile_summary.json + profile_summary.txt, as flash_attention_forward.py:436-522."""
+BUILD_KEY = "__build__"
+
+
+def build_stamp(summary_by_metric: dict | None = None) -> dict:
+    """Which library the profiled process loaded: its fa_build_id (a hash of the
+    kernel sources, host-only call, no GPU needed), its path, and the profiled
+    kernel's name from the kernel-trace pass when there is one."""
+    from flash_attn_npu_amd import flash_attention_forward as fa
+
+    lib = fa._load_library()
+    stamp = {"fa_build_id": lib.fa_build_id().decode(), "library": os.path.basename(str(fa.library_path()))}
+    for s in (summary_by_metric or {}).values():
+        name = s.get("op", {}).get("OP Type")
+        if s.get("op_name") == PROFILE_OP_NAME and name and name != "n/a":
+            stamp["kernel_name"] = name
+            break
+    return stamp
+
+
+def write_profile_summary_files(root: Path, summary_by_metric: dict, build: dict | None = None):
+    """profile_summary.json + profile_summary.txt, as flash_attention_forward.py:436-522.
+
+    `build` (build_stamp()) goes into the JSON under the key "__build__", which
+    compare_results_plus.py skips (it compares only keys without a leading
+    "__", :492-495, after reading every entry's "kernel" / "l2" dicts, :318-338,
+    so the stamp has no key of those names), and into the first line of the
+    text summary.
+    """
     root = Path(root)
     root.mkdir(parents=True, exist_ok=True)
     json_path = root / "profile_summary.json"
     txt_path = root / "profile_summary.txt"
-    json_path.write_text(json.dumps(summary_by_metric, indent=2))
+    data = dict(summary_by_metric)
+    if build is not None:
+        data[BUILD_KEY] = build
+    json_path.write_text(json.dumps(data, indent=2))
     lines = []
+    if build is not None:
+        lines.append("build: " + ", ".join(f"{k}={v}" for k, v in build.items()))
+        lines.append("")
     for metric, s in summary_by_metric.items():
         op = s.get("op", {})
         lines.append(f"[{metric}]")
@@ -380,6 +414,17 @@ def summarize_dir(out: Path, plan=None) -> dict:
     return {name: summarize_pass(Path(out) / name) for name in plan if (Path(out) / name).exists()}
 
 
+def read_build_id(summary_txt: Path) -> str | None:
+    """The fa_build_id a text summary was stamped with (None if it carries none)."""
+    for line in Path(summary_txt).read_text().splitlines():
+        if line.startswith("build:"):
+            for item in line[len("build:"):].split(","):
+                key, _, val = item.strip().partition("=")
+                if key == "fa_build_id":
+                    return val
+    return None
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -398,7 +443,9 @@ def main(argv=None):
         summary = run_passes(Path(args.out), target, plan)
     else:
         summary = summarize_dir(Path(args.out))
-    j, t = write_profile_summary_files(Path(args.out), summary)
+    # The library the target loaded: the one this process resolves the same way
+    # (FA_MI355X_LIB or the in-tree build).
+    j, t = write_profile_summary_files(Path(args.out), summary, build_stamp(summary))
     print(t.read_text())
     print(f"wrote {j} and {t}")
 

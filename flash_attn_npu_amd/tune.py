@@ -289,9 +289,12 @@ def tune_case(module, vendor, case: Case, opts) -> dict:
     if min(statistics.median(xs) for xs in per.values()) < opts.graph_below_us:
         # A launch this short is shorter than the host's per-call cost: back-to-back
         # eager launches then time the host.  Rank the device time of graph replays.
+        # A captured launch walks the static tile schedule (no queue counters), which
+        # for these short grids (at most a few tiles per workgroup) is the eager
+        # order up to the pulls of workgroups that finish early; the label says so.
         graphs = {tag: graph_per_launch(fn, opts.launches) for tag, fn in fns.items()}
         per = time_candidates(fns, opts.rounds, opts.launches, graphs)
-        timing = "graph"
+        timing = "graph (static schedule)"
         del graphs
     for tag, xs in per.items():
         rows[tag].update(avg_us=statistics.median(xs), min_us=min(xs), max_us=max(xs), rounds_us=xs,

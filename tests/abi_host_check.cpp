@@ -187,6 +187,31 @@ int main() {
           CHECK(fa_validate(&p) == FA_ERR_TILING, "odd tiling accepted");
         }
 
+  // Slices near the 2 GiB limit: sequence lengths up to INT32_MAX with seq
+  // strides just below 2^31 elements (the slice-size product exceeds int64).
+  {
+    const int64_t big_strides[] = {(int64_t)(1u << 31) - 8, (int64_t)1 << 30, 1 << 20, 128};
+    const int big_seqs[] = {INT32_MAX, INT32_MAX - 1, 1 << 30, 1 << 24, 1000};
+    for (int64_t ss : big_strides)
+      for (int sk : big_seqs)
+        for (int which = 0; which < 2; ++which) {
+          fa_fwd_params p = valid_params(1, 1, 64, 128, 1, 1);
+          if (which == 0) {
+            p.Sk = sk;
+            p.k_stride[2] = ss;
+            p.v_stride[2] = ss;
+          } else {
+            p.Sq = sk;
+            p.q_stride[2] = ss;
+            p.o_stride[2] = ss;
+          }
+          const int v = fa_validate(&p);
+          const bool fits = ((__int128)((int64_t)sk + 1024) * (ss > 128 ? ss : 128) * 2) < ((__int128)1 << 31);
+          CHECK(v == (fits ? FA_OK : FA_ERR_SHAPE), "S %d stride %lld: %d", sk, (long long)ss, v);
+          check_params(p, rows, nk);
+        }
+  }
+
   // Seeded random sweep over every field, including limits and garbage.
   for (int it = 0; it < 200000; ++it) {
     fa_fwd_params p = valid_params(1 + (int)(next_u64() % 8), 1 + (int)(next_u64() % 40),

@@ -463,3 +463,16 @@ def test_static_split_argument_errors_before_launch(lib):
     assert lib.fa_split_workspace_bytes(ctypes.byref(p), 3) > 32 * 1024 * 1024
     assert lib.fa_fwd_split_static(ctypes.byref(p), 3, None) == -10
     assert b"static scratch" in lib.fa_error_string(-10)
+
+
+def test_call_key_follows_preset_tables(monkeypatch):
+    # The fast-path key changes when a preset table is edited or replaced.
+    from flash_attn_npu_amd import flash_attention_forward as fa
+    q = torch.zeros((1, 2, 16, 64), dtype=torch.float16)
+    k0 = fa._call_key(q, q, q, True, None, None)
+    assert fa._call_key(q, q, q, True, None, None) == k0
+    monkeypatch.setitem(fa.DEFAULT_TILING_PRESETS_BF16, (1, 2, 16, 64, True), (128, 32))
+    k1 = fa._call_key(q, q, q, True, None, None)
+    assert k1 != k0
+    monkeypatch.setattr(fa, "DEFAULT_TILING_PRESETS", dict(fa.DEFAULT_TILING_PRESETS))
+    assert fa._call_key(q, q, q, True, None, None) != k1

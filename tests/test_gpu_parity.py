@@ -208,6 +208,28 @@ def test_repeated_calls_take_the_fast_path(fa, monkeypatch):
         fa.attention(q, k, v, True, float("nan"))
 
 
+def test_fast_path_follows_preset_changes(fa, monkeypatch):
+    """A preset added for a configuration already on the fast path takes effect on the
+    next call (the reference reads its presets on every call), as does replacing a table."""
+    g = torch.Generator().manual_seed(22)
+    B, H, S, D = 1, 2, 260, 64
+    q, k, v = (torch.randn((B, H, S, D), generator=g).to(torch.float16).cuda() for _ in range(3))
+    o64, _ = attention_fp64(q, k, v, False, 0.125)
+    fa._FAST_PLANS.clear()
+    first = fa.attention(q, k, v, False, 0.125)
+    (plan,) = fa._FAST_PLANS.values()
+    default_bn = plan.params.block_n
+    other_bn = 32 if default_bn != 32 else 64
+    monkeypatch.setitem(fa.DEFAULT_TILING_PRESETS, (B, H, S, D, False), (128, other_bn))
+    second = fa.attention(q, k, v, False, 0.125)
+    assert [p.params.block_n for p in fa._FAST_PLANS.values()][-1] == other_bn
+    monkeypatch.setattr(fa, "DEFAULT_TILING_PRESETS", {})
+    third = fa.attention(q, k, v, False, 0.125)
+    assert [p.params.block_n for p in fa._FAST_PLANS.values()][-1] == default_bn
+    for out in (first, second, third):
+        assert (out.float() - o64.to(torch.float16).float()).abs().max().item() <= O_TOL[torch.float16]
+
+
 @pytest.mark.parametrize("scale", [-0.3, 0.0, 2.5])
 def test_unusual_scales(fa, scale):
     g = torch.Generator().manual_seed(9)

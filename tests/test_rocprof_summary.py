@@ -170,3 +170,42 @@ def test_summary_text_carries_step_and_api_lines(tmp_path, passes):
     # The trace has no correlation ids: launch falls back to every launch call.
     assert "step: computing_us=152.000, free_us=48.000, bubble_us=0.000, preparing_us=0.000" in text
     assert "api: launch_avg_us=3.000, sync_avg_us=8.000" in text
+
+
+def test_build_stamp_in_both_summary_files(tmp_path, passes):
+    # The stamp names the profiled library's build; the comparison tool skips
+    # keys with a leading "__" (compare_results_plus.py:492-495).
+    summary = rocprof.summarize_dir(passes, plan={"KernelTrace": None})
+    stamp = {"fa_build_id": "0123456789abcdef", "library": "libfa_mi355x.so", "kernel_name": KERNEL}
+    j, t = rocprof.write_profile_summary_files(tmp_path / "out", summary, stamp)
+    data = json.loads(j.read_text())
+    assert data[rocprof.BUILD_KEY] == stamp and [k for k in data if not k.startswith("__")] == ["KernelTrace"]
+    assert t.read_text().splitlines()[0].startswith("build: fa_build_id=0123456789abcdef, library=libfa_mi355x.so")
+    assert rocprof.read_build_id(t) == "0123456789abcdef"
+    _, t2 = rocprof.write_profile_summary_files(tmp_path / "plain", summary)
+    assert rocprof.read_build_id(t2) is None
+
+
+def test_build_stamp_of_the_tree_library():
+    # build_stamp() loads the library (host-only call) and names the kernel of
+    # the kernel-trace pass.
+    from flash_attn_npu_amd import flash_attention_forward as fa
+    stamp = rocprof.build_stamp({"KernelTrace": {"op_name": rocprof.PROFILE_OP_NAME, "op": {"OP Type": KERNEL}}})
+    assert stamp["fa_build_id"] == fa._load_library().fa_build_id().decode()
+    assert stamp["kernel_name"] == KERNEL
+    assert not {"kernel", "l2", "op", "step", "api"} & set(stamp)  # read by the comparison tool
+
+
+def test_bench_uses_traffic_of_its_own_build_only(tmp_path, monkeypatch):
+    import bench
+    body = ("[HBMRead]\nkernel_metrics: hbm_read_bytes=1000.000, x=1\n[HBMWrite]\n"
+            "kernel_metrics: hbm_write_bytes=24.000\n")
+    prof = tmp_path / "fa_fwd_w_rocprof.txt"
+    monkeypatch.setattr(bench, "profile_summary_path", lambda tag: prof)
+    assert bench.read_traffic("w", "aaaa") is None                      # no summary
+    prof.write_text("# header\n\n" + body)
+    assert bench.read_traffic("w", "aaaa") is None                      # no stamp
+    prof.write_text("build: fa_build_id=bbbb, library=x.so\n\n" + body)
+    assert bench.read_traffic("w", "aaaa") is None                      # another build
+    prof.write_text("# header\n\nbuild: fa_build_id=aaaa, library=x.so\n\n" + body)
+    assert bench.read_traffic("w", "aaaa") == 1024

@@ -84,3 +84,69 @@ def test_static_split_rejects_oversize(fa):
     assert lib.fa_split_workspace_bytes(ctypes.byref(p), 3) > FA_STATIC_SCRATCH_BYTES
     assert lib.fa_fwd_split_static(ctypes.byref(p), 3, fa._current_raw_stream(0)) == FA_ERR_SCRATCH
     assert lib.fa_fwd_split_static(ctypes.byref(p), 0, fa._current_raw_stream(0)) == -9
+
+
+def _capture(lib, p, splits, stream_of):
+    """A CUDA/HIP graph holding one fa_fwd_split_static launch."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = lib.fa_fwd_split_static(ctypes.byref(p), splits, stream_of())
+    assert rc == 0, lib.fa_error_string(rc)
+    return g
+
+
+def test_static_split_in_graph_capture(fa):
+    # The entry point's launches recorded into a graph (no counters, no
+    # allocation, no memset): every replay, with eager calls of the
+    # workspace entry point between them, equals the eager result bit for bit.
+    lib = fa._load_library()
+    dtype, causal, shape, splits = torch.bfloat16, True, (1, 4, 1200, 128), 3
+    print(f"[no-alloc graph] {shape} {dtype} causal={causal} splits={splits}", flush=True)
+    q, k, v = _inputs(41, shape, dtype)
+    scale = shape[3] ** -0.5
+    (o_ws, l_ws), _ = _run_pair(fa, lib, q, k, v, causal, scale, splits)
+    o = torch.full_like(q, float("nan"))
+    lse = torch.full(q.shape[:3], float("nan"), device=q.device, dtype=torch.float32)
+    p = _params(fa, q, k, v, o, lse, causal, scale)
+    g = _capture(lib, p, splits, lambda: fa._current_raw_stream(q.device.index))
+    for r in range(3):
+        o.fill_(float("nan"))
+        lse.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_ws) and torch.equal(lse, l_ws), f"replay {r}"
+        _run_pair(fa, lib, q, k, v, causal, scale, splits)  # eager work between replays
+
+
+_CHILD = r"""
+import ctypes, sys
+import torch
+sys.path.insert(0, sys.argv[1])
+sys.path.insert(0, sys.argv[1] + "/tests")
+from flash_attn_npu_amd import flash_attention_forward as fa
+import test_zz_no_alloc as t
+lib = fa._load_library()
+q, k, v = t._inputs(43, (1, 2, 900, 64), torch.float16)
+o = torch.empty_like(q)
+lse = torch.empty(q.shape[:3], device="cuda", dtype=torch.float32)
+p = t._params(fa, q, k, v, o, lse, False, 0.125)
+# The first call of the library on this device is the captured one.
+g = t._capture(lib, p, 2, lambda: fa._current_raw_stream(0))
+g.replay(); g.replay()
+torch.cuda.synchronize()
+(o_ws, l_ws), _ = t._run_pair(fa, lib, q, k, v, False, 0.125, 2)
+assert torch.equal(o, o_ws) and torch.equal(lse, l_ws)
+print("CAPTURE-FIRST-OK", flush=True)
+"""
+
+
+def test_static_split_first_call_inside_capture():
+    # In a fresh process the entry point resolves its device buffer on its
+    # first call on a device; here that call is being captured.
+    import subprocess
+    import sys
+    from pathlib import Path
+    repo = str(Path(__file__).resolve().parent.parent)
+    print("[no-alloc graph] first library call inside a capture (child process)", flush=True)
+    proc = subprocess.run([sys.executable, "-c", _CHILD, repo], capture_output=True, text=True, timeout=300)
+    assert proc.returncode == 0 and "CAPTURE-FIRST-OK" in proc.stdout, proc.stdout[-2000:] + proc.stderr[-3000:]
