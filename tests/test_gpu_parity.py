@@ -152,6 +152,25 @@ def test_other_head_dims_at_scale(fa, shape, dtype):
     assert (lse.double() - l64).abs().max().item() <= LSE_TOL
 
 
+@pytest.mark.parametrize("shape", [(48, 64, 17, 64, True), (16, 128, 40, 128, False), (8, 96, 130, 128, True),
+                                   (64, 40, 3, 32, False)],
+                         ids=lambda s: "x".join(map(str, s[:4])) + ("c" if s[4] else "f"))
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_many_heads_short_sequences(fa, shape, dtype):
+    """Thousands of (head, m-tile) units of one or two short tiles each (ragged m-tiles of
+    3-130 rows): every workgroup of the persistent grid draws many tickets in quick
+    succession.  All heads vs float64."""
+    z, h, s, d, causal = shape
+    _say(f"[many heads] {shape} {DT_NAME[dtype]}")
+    g = torch.Generator().manual_seed(91 + s)
+    q, k, v = (torch.randn((z, h, s, d), generator=g).to(dtype).cuda() for _ in range(3))
+    scale = 1.0 / math.sqrt(d)
+    out, lse = fa.attention(q, k, v, causal, scale, return_lse=True)
+    o64, l64 = attention_fp64(q, k, v, causal, scale)
+    assert (out.float() - o64.to(dtype).float()).abs().max().item() <= O_TOL[dtype]
+    assert (lse.double() - l64).abs().max().item() <= LSE_TOL
+
+
 def test_strided_inputs_read_in_place(fa):
     """q/k/v as [B,S,H,D] buffers viewed as BNSD (seq stride H*D): no copy needed."""
     g = torch.Generator().manual_seed(7)
