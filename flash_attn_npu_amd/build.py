@@ -24,6 +24,9 @@ PLAN_SRC = PKG_DIR / "csrc" / "fa_plan.cpp"  # included by fa_fwd.hip
 INCLUDE_DIR = REPO_DIR / "include"
 LIB_NAME = "libfa_mi355x.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+# Standalone probe of the sustained dense bf16 MFMA rate (a roofline reference point).
+PROBE_SRC = PKG_DIR / "csrc" / "mfma_ceiling.hip"
+PROBE_PATH = PKG_DIR / "mfma_ceiling"
 OFFLOAD_ARCH = os.environ.get("FA_OFFLOAD_ARCH", "gfx950")
 
 
@@ -86,5 +89,19 @@ def build_library(verbose: bool = False) -> Path:
     return LIB_PATH
 
 
+def build_probe() -> Path:
+    """Compile the MFMA-rate probe executable (always; replaced atomically)."""
+    tmp = PROBE_PATH.with_name(PROBE_PATH.name + ".tmp")
+    cmd = [hipcc_path(), f"--offload-arch={OFFLOAD_ARCH}", "-O3", "-std=c++17",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-Wno-unused-command-line-argument", "-o", str(tmp), str(PROBE_SRC)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr}")
+    os.replace(tmp, PROBE_PATH)
+    return PROBE_PATH
+
+
 if __name__ == "__main__":
     print(build_library(verbose=True))
+    print(build_probe())

@@ -1,0 +1,125 @@
+// mfma_ceiling: the dense bf16 MFMA rate that this GPU sustains, as a
+// reference point for the attention kernel's roofline.
+//
+// Every SIMD runs two waves of back-to-back v_mfma_f32_32x32x16_bf16: four
+// independent accumulator chains per wave, operands rotating over 16 register
+// pairs loaded once from a buffer of random bf16 values (or zeros).  No memory
+// traffic and no other instruction inside the loop, so the rate is bounded only
+// by the matrix cores and by the clock the board allows under that load.  Each
+// wave also stamps s_memtime (shader clock) and s_memrealtime (100 MHz) around
+// its loop, from which the mean shader clock of the run follows.
+//
+//     flash_attn_npu_amd/mfma_ceiling [random|zero] [iterations]
+//
+// Built by flash_attn_npu_amd/build.py next to the library.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kWgPerCu = 2;      // workgroups of 4 waves: 2 waves per SIMD
+constexpr int kThreads = 256;
+constexpr int kPairs = 16;       // operand register pairs per wave
+constexpr size_t kSrcElems = 1u << 20;  // bf16x8 values in the operand buffer (16 MiB)
+
+__global__ void __launch_bounds__(kThreads) mfma_loop(const bf16x8_t *src, float *sink, uint64_t *stamps, int iters) {
+  const int tid = blockIdx.x * blockDim.x + threadIdx.x;
+  bf16x8_t a[kPairs], b[kPairs];
+#pragma unroll
+  for (int i = 0; i < kPairs; ++i) {
+    a[i] = src[(size_t)(tid * 2 * kPairs + i) % kSrcElems];
+    b[i] = src[(size_t)(tid * 2 * kPairs + kPairs + i) % kSrcElems];
+  }
+  f32x16_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+  const uint64_t t0 = __builtin_amdgcn_s_memtime();
+  const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < kPairs; i += 4) {
+      c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[(i * 7) % kPairs], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i + 1], b[(i * 7 + 1) % kPairs], c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i + 2], b[(i * 7 + 2) % kPairs], c2, 0, 0, 0);
+      c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i + 3], b[(i * 7 + 3) % kPairs], c3, 0, 0, 0);
+    }
+  }
+  const uint64_t t1 = __builtin_amdgcn_s_memtime();
+  const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
+  float s = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s += c0[r] + c1[r] + c2[r] + c3[r];
+  sink[tid] = s;  // keeps the loop live
+  if ((threadIdx.x & 63) == 0) {
+    const int w = tid / 64;
+    stamps[2 * w] = t1 - t0;
+    stamps[2 * w + 1] = r1 - r0;
+  }
+}
+
+static int check(hipError_t e, const char *what) {
+  if (e != hipSuccess) {
+    fprintf(stderr, "%s: %s\n", what, hipGetErrorString(e));
+    return 1;
+  }
+  return 0;
+}
+
+int main(int argc, char **argv) {
+  const bool zero = argc > 1 && strcmp(argv[1], "zero") == 0;
+  const int iters = argc > 2 ? atoi(argv[2]) : 1000000;
+  if (iters < 1) {
+    fprintf(stderr, "iterations must be >= 1\n");
+    return 2;
+  }
+  int dev = 0, cus = 0;
+  if (check(hipGetDevice(&dev), "hipGetDevice") ||
+      check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count"))
+    return 1;
+  const int blocks = cus * kWgPerCu;
+  const int waves = blocks * kThreads / 64;
+  bf16x8_t *src = nullptr;
+  float *sink = nullptr;
+  uint64_t *stamps = nullptr;
+  if (check(hipMalloc(&src, kSrcElems * sizeof(bf16x8_t)), "hipMalloc") ||
+      check(hipMalloc(&sink, (size_t)blocks * kThreads * sizeof(float)), "hipMalloc") ||
+      check(hipMalloc(&stamps, (size_t)waves * 2 * sizeof(uint64_t)), "hipMalloc"))
+    return 1;
+  bf16x8_t *host = (bf16x8_t *)malloc(kSrcElems * sizeof(bf16x8_t));
+  uint64_t *hst = (uint64_t *)malloc((size_t)waves * 2 * sizeof(uint64_t));
+  if (host == nullptr || hst == nullptr) return 1;
+  uint32_t lcg = 12345u;  // uniform values in [-1, 1)
+  for (size_t i = 0; i < kSrcElems; ++i)
+    for (int j = 0; j < 8; ++j) {
+      lcg = lcg * 1664525u + 1013904223u;
+      host[i][j] = (__bf16)(zero ? 0.f : ((float)(lcg >> 8) / 16777216.f - 0.5f) * 2.f);
+    }
+  if (check(hipMemcpy(src, host, kSrcElems * sizeof(bf16x8_t), hipMemcpyHostToDevice), "hipMemcpy")) return 1;
+  hipEvent_t e0, e1;
+  if (check(hipEventCreate(&e0), "event") || check(hipEventCreate(&e1), "event")) return 1;
+  hipLaunchKernelGGL(mfma_loop, dim3(blocks), dim3(kThreads), 0, 0, src, sink, stamps, 100);
+  if (check(hipDeviceSynchronize(), "warmup")) return 1;
+  printf("%d CUs, %d waves (2 per SIMD), %s operands, %d iterations of 16 MFMAs per wave\n", cus, waves,
+         zero ? "zero" : "random", iters);
+  for (int rep = 0; rep < 4; ++rep) {
+    (void)hipEventRecord(e0, 0);
+    hipLaunchKernelGGL(mfma_loop, dim3(blocks), dim3(kThreads), 0, 0, src, sink, stamps, iters);
+    (void)hipEventRecord(e1, 0);
+    if (check(hipEventSynchronize(e1), "run")) return 1;
+    float ms = 0.f;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    if (check(hipMemcpy(hst, stamps, (size_t)waves * 2 * sizeof(uint64_t), hipMemcpyDeviceToHost), "stamps"))
+      return 1;
+    double clk = 0.0;
+    for (int w = 0; w < waves; ++w) clk += (double)hst[2 * w] / ((double)hst[2 * w + 1] / 100e6);
+    clk /= waves;
+    const double flops = (double)waves * iters * kPairs * (2.0 * 32 * 32 * 16);
+    printf("run %d: %.1f ms, %.1f TFLOP/s, mean shader clock %.0f MHz\n", rep, ms, flops / (ms * 1e-3) / 1e12,
+           clk / 1e6);
+    fflush(stdout);
+  }
+  return 0;
+}
