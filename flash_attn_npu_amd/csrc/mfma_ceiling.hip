@@ -1,15 +1,19 @@
 // mfma_ceiling: the dense bf16 MFMA rate that this GPU sustains, as a
 // reference point for the attention kernel's roofline.
 //
-// Every SIMD runs two waves of back-to-back v_mfma_f32_32x32x16_bf16: four
-// independent accumulator chains per wave, operands rotating over 16 register
+// Every SIMD runs two waves of back-to-back bf16 MFMAs, either
+// v_mfma_f32_32x32x16_bf16 (four independent accumulator chains per wave, the
+// attention kernel's instruction) or v_mfma_f32_16x16x32_bf16 (eight chains,
+// two instructions per 32x32x16 in FLOPs), operands rotating over 8 register
 // pairs loaded once from a buffer of random bf16 values (or zeros).  No memory
-// traffic and no other instruction inside the loop, so the rate is bounded only
-// by the matrix cores and by the clock the board allows under that load.  Each
-// wave also stamps s_memtime (shader clock) and s_memrealtime (100 MHz) around
-// its loop, from which the mean shader clock of the run follows.
+// traffic and no other instruction inside the loop, so the rate is bounded
+// only by the matrix cores and by the clock the board allows under that load.
+// Each wave also stamps s_memtime (shader clock) and s_memrealtime (100 MHz)
+// around its loop, from which the mean shader clock of the run follows.  The
+// grid is two workgroups per CU; the program refuses to run if the kernel's
+// registers would not let both be resident at once.
 //
-//     flash_attn_npu_amd/mfma_ceiling [random|zero] [iterations]
+//     flash_attn_npu_amd/mfma_ceiling [random|zero] [iterations] [32x32x16|16x16x32]
 //
 // Built by flash_attn_npu_amd/build.py next to the library.
 #include <hip/hip_runtime.h>
@@ -21,13 +25,17 @@
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kWgPerCu = 2;      // workgroups of 4 waves: 2 waves per SIMD
 constexpr int kThreads = 256;
-constexpr int kPairs = 16;       // operand register pairs per wave
+constexpr int kPairs = 8;        // operand register pairs per wave
 constexpr size_t kSrcElems = 1u << 20;  // bf16x8 values in the operand buffer (16 MiB)
+constexpr double kFlopPerIter = 16.0 * 2 * 32 * 32 * 16;  // 16 32x32x16 (or 32 16x16x32) per iteration
 
-__global__ void __launch_bounds__(kThreads) mfma_loop(const bf16x8_t *src, float *sink, uint64_t *stamps, int iters) {
+template <int SHAPE>
+__global__ void __launch_bounds__(kThreads, kWgPerCu) mfma_loop(const bf16x8_t *src, float *sink, uint64_t *stamps,
+                                                                int iters) {
   const int tid = blockIdx.x * blockDim.x + threadIdx.x;
   bf16x8_t a[kPairs], b[kPairs];
 #pragma unroll
@@ -35,23 +43,37 @@ __global__ void __launch_bounds__(kThreads) mfma_loop(const bf16x8_t *src, float
     a[i] = src[(size_t)(tid * 2 * kPairs + i) % kSrcElems];
     b[i] = src[(size_t)(tid * 2 * kPairs + kPairs + i) % kSrcElems];
   }
-  f32x16_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+  float s = 0.f;
   const uint64_t t0 = __builtin_amdgcn_s_memtime();
   const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
-  for (int it = 0; it < iters; ++it) {
+  if constexpr (SHAPE == 32) {
+    f32x16_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int it = 0; it < iters; ++it) {
 #pragma unroll
-    for (int i = 0; i < kPairs; i += 4) {
-      c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[(i * 7) % kPairs], c0, 0, 0, 0);
-      c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i + 1], b[(i * 7 + 1) % kPairs], c1, 0, 0, 0);
-      c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i + 2], b[(i * 7 + 2) % kPairs], c2, 0, 0, 0);
-      c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i + 3], b[(i * 7 + 3) % kPairs], c3, 0, 0, 0);
+      for (int i = 0; i < 16; i += 4) {
+        c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i % kPairs], b[(i * 3) % kPairs], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(i + 1) % kPairs], b[(i * 3 + 1) % kPairs], c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(i + 2) % kPairs], b[(i * 3 + 2) % kPairs], c2, 0, 0, 0);
+        c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(i + 3) % kPairs], b[(i * 3 + 3) % kPairs], c3, 0, 0, 0);
+      }
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += c0[r] + c1[r] + c2[r] + c3[r];
+  } else {
+    f32x4_t c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i)
+        c[i & 7] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i % kPairs], b[(i * 3 + i / kPairs) % kPairs], c[i & 7], 0,
+                                                           0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += c[j][0] + c[j][1] + c[j][2] + c[j][3];
   }
   const uint64_t t1 = __builtin_amdgcn_s_memtime();
   const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
-  float s = 0.f;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) s += c0[r] + c1[r] + c2[r] + c3[r];
   sink[tid] = s;  // keeps the loop live
   if ((threadIdx.x & 63) == 0) {
     const int w = tid / 64;
@@ -71,14 +93,26 @@ static int check(hipError_t e, const char *what) {
 int main(int argc, char **argv) {
   const bool zero = argc > 1 && strcmp(argv[1], "zero") == 0;
   const int iters = argc > 2 ? atoi(argv[2]) : 1000000;
+  const char *shape_name = argc > 3 ? argv[3] : "32x32x16";
   if (iters < 1) {
     fprintf(stderr, "iterations must be >= 1\n");
     return 2;
   }
-  int dev = 0, cus = 0;
+  const bool small = strcmp(shape_name, "16x16x32") == 0;
+  if (!small && strcmp(shape_name, "32x32x16") != 0) {
+    fprintf(stderr, "shape must be 32x32x16 or 16x16x32\n");
+    return 2;
+  }
+  void (*kern)(const bf16x8_t *, float *, uint64_t *, int) = small ? mfma_loop<16> : mfma_loop<32>;
+  int dev = 0, cus = 0, resident = 0;
   if (check(hipGetDevice(&dev), "hipGetDevice") ||
-      check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count"))
+      check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count") ||
+      check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, kern, kThreads, 0), "occupancy"))
     return 1;
+  if (resident < kWgPerCu) {
+    fprintf(stderr, "only %d workgroups of this kernel fit on a CU, %d needed\n", resident, kWgPerCu);
+    return 1;
+  }
   const int blocks = cus * kWgPerCu;
   const int waves = blocks * kThreads / 64;
   bf16x8_t *src = nullptr;
@@ -100,23 +134,22 @@ int main(int argc, char **argv) {
   if (check(hipMemcpy(src, host, kSrcElems * sizeof(bf16x8_t), hipMemcpyHostToDevice), "hipMemcpy")) return 1;
   hipEvent_t e0, e1;
   if (check(hipEventCreate(&e0), "event") || check(hipEventCreate(&e1), "event")) return 1;
-  hipLaunchKernelGGL(mfma_loop, dim3(blocks), dim3(kThreads), 0, 0, src, sink, stamps, 100);
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), 0, 0, src, sink, stamps, 100);
   if (check(hipDeviceSynchronize(), "warmup")) return 1;
-  printf("%d CUs, %d waves (2 per SIMD), %s operands, %d iterations of 16 MFMAs per wave\n", cus, waves,
-         zero ? "zero" : "random", iters);
+  printf("%d CUs, %d waves (%d per SIMD), v_mfma_f32_%s_bf16, %s operands, %d iterations of %d MFMAs per wave\n",
+         cus, waves, kWgPerCu, shape_name, zero ? "zero" : "random", iters, small ? 32 : 16);
   for (int rep = 0; rep < 4; ++rep) {
-    (void)hipEventRecord(e0, 0);
-    hipLaunchKernelGGL(mfma_loop, dim3(blocks), dim3(kThreads), 0, 0, src, sink, stamps, iters);
-    (void)hipEventRecord(e1, 0);
-    if (check(hipEventSynchronize(e1), "run")) return 1;
+    if (check(hipEventRecord(e0, 0), "event record")) return 1;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), 0, 0, src, sink, stamps, iters);
+    if (check(hipEventRecord(e1, 0), "event record") || check(hipEventSynchronize(e1), "run")) return 1;
     float ms = 0.f;
-    (void)hipEventElapsedTime(&ms, e0, e1);
+    if (check(hipEventElapsedTime(&ms, e0, e1), "elapsed")) return 1;
     if (check(hipMemcpy(hst, stamps, (size_t)waves * 2 * sizeof(uint64_t), hipMemcpyDeviceToHost), "stamps"))
       return 1;
     double clk = 0.0;
     for (int w = 0; w < waves; ++w) clk += (double)hst[2 * w] / ((double)hst[2 * w + 1] / 100e6);
     clk /= waves;
-    const double flops = (double)waves * iters * kPairs * (2.0 * 32 * 32 * 16);
+    const double flops = (double)waves * iters * kFlopPerIter;
     printf("run %d: %.1f ms, %.1f TFLOP/s, mean shader clock %.0f MHz\n", rep, ms, flops / (ms * 1e-3) / 1e12,
            clk / 1e6);
     fflush(stdout);
