@@ -19,7 +19,7 @@ seeds (`seed + idx`), tolerances, paired alternating timing and scoring:
 
 A third suite, `configs`, runs the five benchmark workloads
 (flash_attn_npu_amd/workloads.py) against a float64 device restatement with
-the north-star gates (O <= 5e-3 fp16 / 2e-2 bf16, LSE <= 1e-3).
+the workloads' accuracy gates (O <= 5e-3 fp16 / 2e-2 bf16, LSE <= 1e-3).
 
 Reports: `evaluation_report.json` / `.txt` in --report-dir with the reference
 schema (evaluate_attention.py:425-507); the `configs` suite adds one key.
