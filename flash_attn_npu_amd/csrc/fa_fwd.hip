@@ -1166,9 +1166,83 @@ fa_fwd_dma_kernel(KernelArgs p) {
       buf_store4(__builtin_bit_cast(uint32_t, lse), rpl, h ? nbytes : (uint32_t)qrow * 4u);
     } else {
     const float inv = 1.f / l_tot;
-    {
-      const char *og = p.o + 2 * (bb * p.o_sb + hh * p.o_sh);
-      const BufRsrc ro = make_rsrc(og, (uint32_t)((int64_t)p.Sq * p.o_ss * 2));
+    const char *og = p.o + 2 * (bb * p.o_sb + hh * p.o_sh);
+    const BufRsrc ro = make_rsrc(og, (uint32_t)((int64_t)p.Sq * p.o_ss * 2));
+    // A lane holds 4-dim pieces of one row of O (the O^T layout), so storing
+    // them directly makes every store instruction touch 32 rows.  Staged
+    // stores send O through LDS instead, and each instruction writes whole
+    // rows: the wave writes its 32 rows into the 1 KB LDS chunks that only
+    // its own DMAs fill, in the stage that received the last tile's (empty)
+    // DMAs.  Those have landed (vmcnt above), no other wave reads that stage
+    // after the last tile's barrier, and the next unit's DMAs wait for the
+    // barrier at the end of this unit.  It then reads them back one chunk per
+    // instruction and stores 16 bytes per lane along the rows.  Kernels whose
+    // DMAs fill fewer chunks than 32 rows take (32-key tiles, 64-key fp8 V)
+    // run two passes over the halves of the head dims; 16-byte units of a row
+    // are XOR-swizzled by the row, so the 32 rows of a write spread over the
+    // banks.  The D = 128 kernels at three workgroups per CU keep the direct
+    // stores: their 168-register budget has no room for the staging (2
+    // registers spilled).
+    constexpr bool kStagedStore = !(D >= 128 && OCC >= 3);
+    if constexpr (kStagedStore) {
+      constexpr int kOwn = C::NDMA;          // 1 KB chunks this wave's DMAs fill
+      constexpr int kNeed = D / 16;          // KB of 32 rows of 2 D bytes
+      constexpr int NPASS = kOwn >= kNeed ? 1 : 2;
+      static_assert(NPASS * kOwn >= kNeed && (NPASS == 1 || C::DB % 2 == 0), "O staging space");
+      constexpr int W = 2 * D / NPASS;       // bytes of a row per pass
+      constexpr int RPC = 1024 / W;          // rows per chunk
+      constexpr int U = W / 16;              // 16-byte units per row segment
+      constexpr int USW = U < 32 ? U : 32;   // swizzle span
+      constexpr int DBP = C::DB / NPASS;
+      constexpr int JN = D >= 32 ? 4 : 2;
+      constexpr int NR = 32 / RPC;           // chunks per pass
+      constexpr int RG = NR < 4 ? NR : 4;    // chunks read per group
+      char *const fs = (n_tiles & 1) ? smem1 : smem0;
+      // Lane and wave indices made opaque here, so that the addresses below
+      // (which depend on nothing else) are not hoisted out of the unit loop
+      // and kept live through every tile.
+      int ln = lane, wv = wave;
+      asm volatile("" : "+v"(ln), "+s"(wv));
+      const int ln_n = ln & 31, ln_h = ln >> 5;
+      auto own = [&](int k) __attribute__((always_inline)) {
+        return k < C::IPW ? (uint32_t)((wv + k * NW) * 1024)
+                          : (uint32_t)(C::TILE + (wv + (k - C::IPW) * NW) * 1024);
+      };
+      const uint32_t wbase = own(ln_n / RPC) + (uint32_t)((ln_n % RPC) * W + 8 * ln_h);
+      const int wsw = ln_n & (USW - 1);
+      const int rr = ln / U, lu = ln % U;
+      // Scheduling barriers keep the writes of one block, and the reads of
+      // four chunks, apart from the next ones: hoisted together they would
+      // hold every packed row or read chunk in registers at once.
+#pragma unroll
+      for (int ps = 0; ps < NPASS; ++ps) {
+#pragma unroll
+        for (int db = ps * DBP; db < (ps + 1) * DBP; ++db) {
+#pragma unroll
+          for (int j = 0; j < JN; ++j) {  // dims 32db + 8j + 4h + 0..3: unit 4 (db - ps DBP) + j, half h
+            u32x2_t x;
+            x[0] = pack2<BF16>(oacc[db][4 * j + 0] * inv, oacc[db][4 * j + 1] * inv);
+            x[1] = pack2<BF16>(oacc[db][4 * j + 2] * inv, oacc[db][4 * j + 3] * inv);
+            const int u = 4 * (db - ps * DBP) + j;
+            *(u32x2_t *)(fs + wbase + ((u ^ wsw) << 4)) = x;
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int r0 = 0; r0 < NR; r0 += RG) {
+          u32x4_t x[RG];
+#pragma unroll
+          for (int i = 0; i < RG; ++i) {
+            const int row = (r0 + i) * RPC + rr;
+            x[i] = *(const u32x4_t *)(fs + own(r0 + i) + rr * W + ((lu ^ (row & (USW - 1))) << 4));
+          }
+#pragma unroll
+          for (int i = 0; i < RG; ++i)
+            buf_store16(x[i], ro, (uint32_t)((q0w + (r0 + i) * RPC + rr) * p.o_ss * 2 + ps * W + lu * 16));
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else {
       const uint32_t oo = (uint32_t)(qrow * p.o_ss * 2 + 8 * h);
 #pragma unroll
       for (int db = 0; db < C::DB; ++db)
