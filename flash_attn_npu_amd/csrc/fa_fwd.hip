@@ -622,25 +622,80 @@ fa_fwd_dma_kernel(KernelArgs p) {
       }
     };
 
-    // Prologue: KV tile t_begin into its stage (t_begin & 1).
-    {
+    // Prologue: KV tile t_begin into its stage (t_begin & 1), and this wave's
+    // Q rows.
+    auto kv_prologue = [&](auto stage_tag) __attribute__((always_inline)) {
       BufRsrc rk, rv;
       tile_rsrc(t_begin, &rk, &rv);
-      if (t_begin & 1) {
 #pragma unroll
-        for (int i = 0; i < C::NDMA; ++i) dma(std::integral_constant<int, 1>{}, rk, rv, i);
-      } else {
-#pragma unroll
-        for (int i = 0; i < C::NDMA; ++i) dma(std::integral_constant<int, 0>{}, rk, rv, i);
-      }
-    }
-
+      for (int i = 0; i < C::NDMA; ++i) dma(stage_tag, rk, rv, i);
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
     u32x4_t qf[D / 16];
     {
       const BufRsrc rq = make_rsrc(qg, (uint32_t)((int64_t)p.Sq * p.q_ss * 2));
-      const uint32_t qo = (uint32_t)(qrow * p.q_ss * 2 + 16 * h);
+      // A lane's Q fragment s is 16 bytes of its own row (bytes 32s + 16h),
+      // so loading fragments directly makes every load instruction touch 32
+      // rows.  Where the 1 KB LDS chunks that this wave's DMAs fill hold its
+      // 32 rows, Q comes through them instead: DMAs that each read 1 KB of
+      // whole rows, into the stage that tile t_begin does not use (free until
+      // the first tile's DMAs, which this wave issues after the reads below
+      // have completed; other waves' DMAs fill only their own chunks), then
+      // one LDS read per fragment.  16-byte units of a row sit XOR-swizzled
+      // by the row, so the 32 rows of a read spread over the banks.  The Q
+      // DMAs go first so that waiting for them leaves the K/V DMAs in flight
+      // (vmcnt retires in issue order).  At three or more workgroups per CU
+      // the others hide a unit's prologue and the staging measured 1% slower
+      // (B16 H16 S1024 D64), so those kernels load Q directly, as do the
+      // kernels whose chunks hold fewer rows (a separate 64 KB Q area for the
+      // 32-key D = 256 kernels measured 1-2% slower).
+      constexpr bool kQOwn = C::NDMA >= D / 16 && OCC <= 2;
+      constexpr int W = 2 * D;                                 // bytes per row
+      constexpr int RPC = 1024 / W;                            // rows per chunk
+      constexpr int U = W / 16;                                // 16-byte units per row
+      constexpr int USW = U < 32 ? U : 32;                     // swizzle span
+      // Q rows of this wave into 1 KB chunks chunk(k) (k < 32 / RPC), the
+      // K/V DMAs of tile t_begin behind them, then the fragments from LDS.
+      auto q_staged = [&](auto chunk, int ln, auto kv_tag) __attribute__((always_inline)) {
+        const int rr = ln / U, slot = ln % U;
 #pragma unroll
-      for (int s = 0; s < D / 16; ++s) qf[s] = buf_load16(rq, qo + 32 * s) ^ p.q_sign;
+        for (int k = 0; k < 32 / RPC; ++k) {  // chunk k: rows k RPC .. + RPC, lane -> (row, slot)
+          const int row = k * RPC + rr;
+          dma16_lds(rq, chunk(k), (uint32_t)((q0w + row) * p.q_ss * 2 + ((slot ^ (row & (USW - 1))) << 4)));
+        }
+        kv_prologue(kv_tag);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(C::NDMA));
+        const int ln_n = ln & 31, ln_h = ln >> 5;
+        const char *const rb = chunk(ln_n / RPC) + (ln_n % RPC) * W;
+        const int sw = ln_n & (USW - 1);
+#pragma unroll
+        for (int s = 0; s < D / 16; ++s) qf[s] = *(const u32x4_t *)(rb + (((2 * s + ln_h) ^ sw) << 4)) ^ p.q_sign;
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): reads done before the chunks take DMAs again
+      };
+      if constexpr (kQOwn) {
+        int ln = lane, wv = wave;  // opaque: keeps the addresses in the prologue
+        asm volatile("" : "+v"(ln), "+s"(wv));
+        auto run_q = [&](auto q_tag, auto kv_tag) __attribute__((always_inline)) {
+          char *const qb = decltype(q_tag)::value == 0 ? smem0 : smem1;
+          auto chunk = [&](int k) __attribute__((always_inline)) {
+            return qb + (k < C::IPW ? (wv + k * NW) * 1024 : C::TILE + (wv + (k - C::IPW) * NW) * 1024);
+          };
+          q_staged(chunk, ln, kv_tag);
+        };
+        if (t_begin & 1)
+          run_q(S0{}, S1{});
+        else
+          run_q(S1{}, S0{});
+      } else {
+        if (t_begin & 1)
+          kv_prologue(S1{});
+        else
+          kv_prologue(S0{});
+        const uint32_t qo = (uint32_t)(qrow * p.q_ss * 2 + 16 * h);
+#pragma unroll
+        for (int s = 0; s < D / 16; ++s) qf[s] = buf_load16(rq, qo + 32 * s) ^ p.q_sign;
+      }
       // One workgroup per CU (D = 256, 16-bit V): Q lives in AGPRs (the MFMA
       // reads its B operand from there), which leaves the VGPRs to S, P and the
       // fragments.  (With fp8 V the 64-key S block takes those AGPRs.)
@@ -1063,8 +1118,6 @@ fa_fwd_dma_kernel(KernelArgs p) {
     // Tiles visible to every query of the workgroup need no mask.  Each run
     // of tiles steps t in stage pairs (t even -> stage 0).
     const int n_full = n_full_of(q0);
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
     using NotFirst = std::integral_constant<bool, false>;
     int t = t_begin;
     auto run = [&](int end, auto masked_tag) __attribute__((always_inline)) {
