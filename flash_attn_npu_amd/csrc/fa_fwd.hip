@@ -723,12 +723,17 @@ fa_fwd_dma_kernel(KernelArgs p) {
     // the mask (and for skipping tiles above a wave's own rows), and neither
     // loop body branches on it.  STG = t % 2 is compile-time too, so every
     // LDS read address is a per-lane base plus an immediate offset.
-    auto kv_tile = [&](int t, auto masked_tag, auto stage_tag, auto exact_tag) __attribute__((always_inline)) {
+    auto kv_tile = [&](int t, auto masked_tag, auto stage_tag, auto exact_tag,
+                       auto half_tag) __attribute__((always_inline)) {
       constexpr bool MASKED = decltype(masked_tag)::value;
       constexpr int STG = decltype(stage_tag)::value;
       constexpr bool EXACT = decltype(exact_tag)::value;  // the unit's first tile
       // Tiles after the first of 64 keys (16-bit V) take the block-split body.
       constexpr bool SPLIT = kSumTrigger && !EXACT && !V8 && BN == 64;
+      // HALF: a masked tile whose second 32-key block lies past every row of
+      // this wave (causal), so only the first block is computed.
+      constexpr bool HALF = decltype(half_tag)::value;
+      static_assert(!HALF || (SPLIT && MASKED), "half tiles take the block-split masked body");
 #ifdef FA_TIMING
       const uint32_t ta = FA_CLK();
       if (t == 0) tm_pro = ta - tm0;
@@ -881,6 +886,40 @@ fa_fwd_dma_kernel(KernelArgs p) {
         // Number of softmax VALU instructions placed after each MFMA.
         constexpr int kValuPerMfma = 7;
         constexpr int kSchedValu = 0x002 | 0x400;  // VALU and TRANS
+        constexpr int NPVB = 2 * C::DB;  // P.V MFMAs per block
+
+        if constexpr (HALF) {
+          // Block 1 is masked for every row of the wave: its p are 0 and it
+          // adds nothing to l or O, so block 0 alone gives the same result.
+          // The tile's DMAs still go out, one per QK MFMA.
+          static_assert(C::NDMA <= NS, "one DMA per QK MFMA of block 0");
+          constexpr int VAT = NS - 1;  // V^T reads at the last QK step (fewer live fragments)
+#pragma unroll
+          for (int i = 0; i < KPF && i < NS; ++i) kfr[i] = kread_b(i);
+#pragma unroll
+          for (int i = 0; i < NS; ++i) {
+            if (i + KPF < NS) kfr[i + KPF] = kread_b(i + KPF);
+            if (i == VAT) {
+#pragma unroll
+              for (int j = 0; j < VPF; ++j) vfr[j] = vread(j);
+            }
+            sacc[0] = mfma32x32x16<BF16>(kfr[i], qf[i], sacc[0]);
+            if (i < NDMA) dma(NEXT{}, rk_n, rv_n, i);
+          }
+          mask_block(0);
+          exps_block(0, m_run);
+          settle_block(0);
+          if constexpr (D >= 128) __builtin_amdgcn_s_setprio(1);
+          pack_block(0);
+#pragma unroll
+          for (int i = 0; i < NPVB; ++i) {
+            if (i + VPF < NPVB) vfr[i + VPF] = vread(i + VPF);
+            const int ks = i / C::DB, db = i % C::DB;
+            oacc[db] = mfma32x32x16<BF16>(vfr[i], pf[ks], oacc[db]);
+          }
+          if constexpr (D >= 128) __builtin_amdgcn_s_setprio(0);
+          return;
+        }
 
         // S^T = K Q^T block by block (reads KPF ahead, one DMA per MFMA),
         // block 0's softmax under block 1's MFMAs.
@@ -914,7 +953,6 @@ fa_fwd_dma_kernel(KernelArgs p) {
         // softmax between the MFMAs, then block 1's keys.
         if constexpr (D >= 128) __builtin_amdgcn_s_setprio(1);
         pack_block(0);
-        constexpr int NPVB = 2 * C::DB;  // P.V MFMAs per block
 #pragma unroll
         for (int i = 0; i < NPVB; ++i) {
           vfr[i + VPF] = vread(i + VPF);
@@ -1119,22 +1157,23 @@ fa_fwd_dma_kernel(KernelArgs p) {
     // of tiles steps t in stage pairs (t even -> stage 0).
     const int n_full = n_full_of(q0);
     using NotFirst = std::integral_constant<bool, false>;
+    using Whole = std::integral_constant<bool, false>;
     int t = t_begin;
     auto run = [&](int end, auto masked_tag) __attribute__((always_inline)) {
-      if (t < end && (t & 1)) kv_tile(t++, masked_tag, S1{}, NotFirst{});
+      if (t < end && (t & 1)) kv_tile(t++, masked_tag, S1{}, NotFirst{}, Whole{});
       for (; t + 1 < end; t += 2) {
-        kv_tile(t, masked_tag, S0{}, NotFirst{});
-        kv_tile(t + 1, masked_tag, S1{}, NotFirst{});
+        kv_tile(t, masked_tag, S0{}, NotFirst{}, Whole{});
+        kv_tile(t + 1, masked_tag, S1{}, NotFirst{}, Whole{});
       }
-      if (t < end) kv_tile(t++, masked_tag, S0{}, NotFirst{});
+      if (t < end) kv_tile(t++, masked_tag, S0{}, NotFirst{}, Whole{});
     };
     // The unit's first tile (it sets the running max), in its stage.
     auto first_tile = [&](auto masked_tag) __attribute__((always_inline)) {
       using First = std::integral_constant<bool, true>;
       if (t & 1)
-        kv_tile(t, masked_tag, S1{}, First{});
+        kv_tile(t, masked_tag, S1{}, First{}, Whole{});
       else
-        kv_tile(t, masked_tag, S0{}, First{});
+        kv_tile(t, masked_tag, S0{}, First{}, Whole{});
       ++t;
     };
     // Tiles [t, end) in which this wave has nothing to compute: only keep the
@@ -1180,8 +1219,24 @@ fa_fwd_dma_kernel(KernelArgs p) {
         else if (t < n_act)
           first_tile(Masked{});
       }
+      // Causal: when the wave's rows end in the first 32 keys of its last
+      // tile (and that tile is masked and not the unit's first), the second
+      // block is masked for all of them and the tile runs as a half tile.
+      constexpr bool kHalfTiles = CAUSAL && OCC >= 2 && kSumTrigger && !V8 && BN == 64;
+      const bool half_last =
+          kHalfTiles && n_act - 1 > max(n_full - 1, t_begin) && wave_last_q - (n_act - 1) * BN < 32;
       run(n_full, Unmasked{});
-      run(n_act, Masked{});
+      run(half_last ? n_act - 1 : n_act, Masked{});
+      if constexpr (kHalfTiles) {
+        if (half_last) {
+          using Half = std::integral_constant<bool, true>;
+          if (t & 1)
+            kv_tile(t, Masked{}, S1{}, NotFirst{}, Half{});
+          else
+            kv_tile(t, Masked{}, S0{}, NotFirst{}, Half{});
+          ++t;
+        }
+      }
       idle_tiles(n_tiles);
     }
 #ifdef FA_TIMING
