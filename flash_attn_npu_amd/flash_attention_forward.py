@@ -61,7 +61,7 @@ DEFAULT_TILING_PRESETS = {
     (128, 8, 1024, 256, True): (128, 32),
     (128, 8, 2048, 128, True): (128, 64),
     (128, 8, 2048, 256, False): (128, 32),
-    (128, 8, 4096, 128, False): (256, 64),
+    (128, 8, 4096, 128, False): (128, 32),
     (128, 8, 8192, 64, False): (128, 64),
 }
 DEFAULT_TILING_PRESETS_BF16 = {
