@@ -8,12 +8,20 @@
 // pairs loaded once from a buffer of random bf16 values (or zeros).  No memory
 // traffic and no other instruction inside the loop, so the rate is bounded
 // only by the matrix cores and by the clock the board allows under that load.
+// Two more 32x32x16 forms answer questions about the tile body:
+//   32x32x16-1chain   one wave per SIMD and a single accumulator chain (every
+//                     MFMA reads the previous one's result as its C input),
+//                     the shape of a 32-key S^T block summed over D;
+//   32x32x16-shareb   the B operand shared by consecutive pairs of MFMAs (as
+//                     the two key blocks of a tile share Q), against the
+//                     default's new A and B on every instruction.
 // Each wave also stamps s_memtime (shader clock) and s_memrealtime (100 MHz)
 // around its loop, from which the mean shader clock of the run follows.  The
-// grid is two workgroups per CU; the program refuses to run if the kernel's
-// registers would not let both be resident at once.
+// grid fills every SIMD with its waves; the program refuses to run if the
+// kernel's registers would not let them be resident at once.
 //
-//     flash_attn_npu_amd/mfma_ceiling [random|zero] [iterations] [32x32x16|16x16x32]
+//     flash_attn_npu_amd/mfma_ceiling [random|zero] [iterations]
+//                                     [32x32x16|16x16x32|32x32x16-1chain|32x32x16-shareb]
 //
 // Built by flash_attn_npu_amd/build.py next to the library.
 #include <hip/hip_runtime.h>
@@ -27,15 +35,16 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kWgPerCu = 2;      // workgroups of 4 waves: 2 waves per SIMD
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;    // workgroups of 4 waves, one per SIMD
 constexpr int kPairs = 8;        // operand register pairs per wave
 constexpr size_t kSrcElems = 1u << 20;  // bf16x8 values in the operand buffer (16 MiB)
 constexpr double kFlopPerIter = 16.0 * 2 * 32 * 32 * 16;  // 16 32x32x16 (or 32 16x16x32) per iteration
 
-template <int SHAPE>
-__global__ void __launch_bounds__(kThreads, kWgPerCu) mfma_loop(const bf16x8_t *src, float *sink, uint64_t *stamps,
-                                                                int iters) {
+// SHAPE 32: 32x32x16 over CHAINS accumulators (SHAREB: B index advances every
+// second MFMA); SHAPE 16: 16x16x32 over eight.  WPS waves per SIMD.
+template <int SHAPE, int CHAINS, bool SHAREB, int WPS>
+__global__ void __launch_bounds__(kThreads, WPS) mfma_loop(const bf16x8_t *src, float *sink, uint64_t *stamps,
+                                                           int iters) {
   const int tid = blockIdx.x * blockDim.x + threadIdx.x;
   bf16x8_t a[kPairs], b[kPairs];
 #pragma unroll
@@ -47,18 +56,20 @@ __global__ void __launch_bounds__(kThreads, kWgPerCu) mfma_loop(const bf16x8_t *
   const uint64_t t0 = __builtin_amdgcn_s_memtime();
   const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
   if constexpr (SHAPE == 32) {
-    f32x16_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    f32x16_t c[CHAINS];
+#pragma unroll
+    for (int j = 0; j < CHAINS; ++j) c[j] = (f32x16_t){};
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
-      for (int i = 0; i < 16; i += 4) {
-        c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i % kPairs], b[(i * 3) % kPairs], c0, 0, 0, 0);
-        c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(i + 1) % kPairs], b[(i * 3 + 1) % kPairs], c1, 0, 0, 0);
-        c2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(i + 2) % kPairs], b[(i * 3 + 2) % kPairs], c2, 0, 0, 0);
-        c3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(i + 3) % kPairs], b[(i * 3 + 3) % kPairs], c3, 0, 0, 0);
+      for (int i = 0; i < 16; ++i) {
+        const int bi = SHAREB ? ((i / 2) * 3 + 1) % kPairs : (3 * (i - i % 4) + i % 4) % kPairs;
+        c[i % CHAINS] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i % kPairs], b[bi], c[i % CHAINS], 0, 0, 0);
       }
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s += c0[r] + c1[r] + c2[r] + c3[r];
+    for (int j = 0; j < CHAINS; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s += c[j][r];
   } else {
     f32x4_t c[8];
 #pragma unroll
@@ -98,22 +109,33 @@ int main(int argc, char **argv) {
     fprintf(stderr, "iterations must be >= 1\n");
     return 2;
   }
-  const bool small = strcmp(shape_name, "16x16x32") == 0;
-  if (!small && strcmp(shape_name, "32x32x16") != 0) {
-    fprintf(stderr, "shape must be 32x32x16 or 16x16x32\n");
+  void (*kern)(const bf16x8_t *, float *, uint64_t *, int) = nullptr;
+  int wps = 2;  // waves per SIMD = workgroups per CU
+  bool small = false;
+  if (strcmp(shape_name, "32x32x16") == 0) {
+    kern = mfma_loop<32, 4, false, 2>;
+  } else if (strcmp(shape_name, "16x16x32") == 0) {
+    kern = mfma_loop<16, 8, false, 2>;
+    small = true;
+  } else if (strcmp(shape_name, "32x32x16-1chain") == 0) {
+    kern = mfma_loop<32, 1, false, 1>;
+    wps = 1;
+  } else if (strcmp(shape_name, "32x32x16-shareb") == 0) {
+    kern = mfma_loop<32, 4, true, 2>;
+  } else {
+    fprintf(stderr, "shape must be 32x32x16, 16x16x32, 32x32x16-1chain or 32x32x16-shareb\n");
     return 2;
   }
-  void (*kern)(const bf16x8_t *, float *, uint64_t *, int) = small ? mfma_loop<16> : mfma_loop<32>;
   int dev = 0, cus = 0, resident = 0;
   if (check(hipGetDevice(&dev), "hipGetDevice") ||
       check(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count") ||
       check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&resident, kern, kThreads, 0), "occupancy"))
     return 1;
-  if (resident < kWgPerCu) {
-    fprintf(stderr, "only %d workgroups of this kernel fit on a CU, %d needed\n", resident, kWgPerCu);
+  if (resident < wps) {
+    fprintf(stderr, "only %d workgroups of this kernel fit on a CU, %d needed\n", resident, wps);
     return 1;
   }
-  const int blocks = cus * kWgPerCu;
+  const int blocks = cus * wps;
   const int waves = blocks * kThreads / 64;
   bf16x8_t *src = nullptr;
   float *sink = nullptr;
@@ -137,7 +159,7 @@ int main(int argc, char **argv) {
   hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), 0, 0, src, sink, stamps, 100);
   if (check(hipDeviceSynchronize(), "warmup")) return 1;
   printf("%d CUs, %d waves (%d per SIMD), v_mfma_f32_%s_bf16, %s operands, %d iterations of %d MFMAs per wave\n",
-         cus, waves, kWgPerCu, shape_name, zero ? "zero" : "random", iters, small ? 32 : 16);
+         cus, waves, wps, shape_name, zero ? "zero" : "random", iters, small ? 32 : 16);
   for (int rep = 0; rep < 4; ++rep) {
     if (check(hipEventRecord(e0, 0), "event record")) return 1;
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(kThreads), 0, 0, src, sink, stamps, iters);
