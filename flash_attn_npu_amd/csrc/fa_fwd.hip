@@ -430,7 +430,12 @@ struct Cfg2 {
   static constexpr int VTILE_LDS = VIPW * NW * 1024;
   static constexpr int NDMA = IPW + VIPW;     // DMA instructions per wave and tile
   static constexpr int STAGE = TILE + VTILE_LDS;
-  static constexpr int LDS_BYTES = NSTAGE * STAGE;
+  // One workgroup per CU, 16-bit V, and fewer DMA chunks per wave than 32 Q
+  // rows fill (the 32-key D = 256 kernels): Q comes in through an LDS area of
+  // its own, BM rows of 2 D bytes.
+  static constexpr bool QAREA = OCC == 1 && !V8 && NDMA < D / 16;
+  static constexpr int Q_BYTES = QAREA ? BM * 2 * D : 0;
+  static constexpr int LDS_BYTES = NSTAGE * STAGE + Q_BYTES;
   // O^T blocks of 32 head dims; D = 16 uses one block whose upper 16 rows
   // come out zero (the V^T operand rows past D are zeroed).
   static constexpr int DB = D >= 32 ? D / 32 : 1;
@@ -471,6 +476,13 @@ fa_fwd_dma_kernel(KernelArgs p) {
   // vmcnt wait in front of them.
   __shared__ __attribute__((aligned(1024))) char smem0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) char smem1[C::STAGE];
+  // Q area (C::QAREA kernels only): the launch's dynamic LDS, which follows
+  // the static arrays, so the stages stay in the low 64 KB where every K and
+  // V^T read is a per-lane base plus an immediate offset (a static area was
+  // placed first and cost the kernel 58 registers of addresses).  Wave w's Q
+  // rows take bytes [32 w, 32 w + 32) x 2 D.  (Staging O there as well, in one
+  // pass instead of two through the stages, measured no faster.)
+  extern __shared__ __attribute__((aligned(1024))) char smemq[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -647,10 +659,13 @@ fa_fwd_dma_kernel(KernelArgs p) {
       // DMAs go first so that waiting for them leaves the K/V DMAs in flight
       // (vmcnt retires in issue order).  At three or more workgroups per CU
       // the others hide a unit's prologue and the staging measured 1% slower
-      // (B16 H16 S1024 D64), so those kernels load Q directly, as do the
-      // kernels whose chunks hold fewer rows (a separate 64 KB Q area for the
-      // 32-key D = 256 kernels measured 1-2% slower).
+      // (B16 H16 S1024 D64), so those kernels load Q directly.  The 32-key
+      // D = 256 kernels, whose chunks hold 16 rows, stage Q the same way
+      // through a Q area of their own (0.2-0.9% faster than direct loads),
+      // and the fp8-V D = 256 kernel, whose stages leave no room for one,
+      // loads it directly.
       constexpr bool kQOwn = C::NDMA >= D / 16 && OCC <= 2;
+      static_assert(!(kQOwn && C::QAREA), "one Q staging area");
       constexpr int W = 2 * D;                                 // bytes per row
       constexpr int RPC = 1024 / W;                            // rows per chunk
       constexpr int U = W / 16;                                // 16-byte units per row
@@ -687,6 +702,17 @@ fa_fwd_dma_kernel(KernelArgs p) {
           run_q(S0{}, S1{});
         else
           run_q(S1{}, S0{});
+      } else if constexpr (C::QAREA) {
+        // The wave's 32 rows in its own part of the Q area: nothing else
+        // writes there, and its next accesses to it follow these reads.
+        int ln = lane, wv = wave;  // opaque: keeps the addresses in the prologue
+        asm volatile("" : "+v"(ln), "+s"(wv));
+        char *const qb = smemq + wv * (32 * W);
+        auto chunk = [&](int k) __attribute__((always_inline)) { return qb + k * 1024; };
+        if (t_begin & 1)
+          q_staged(chunk, ln, S1{});
+        else
+          q_staged(chunk, ln, S0{});
       } else {
         if (t_begin & 1)
           kv_prologue(S1{});
@@ -2040,7 +2066,8 @@ int launch(const fa_fwd_params *p, void *hip_stream, int splits, void *workspace
   a.c = c;
   a.timing = g_timing_buffer;
 
-  hipLaunchKernelGGL(kKernelFns.fns[plan.kernel], dim3(plan.grid), dim3(64 * e.NW), 0, stream, a);
+  hipLaunchKernelGGL(kKernelFns.fns[plan.kernel], dim3(plan.grid), dim3(64 * e.NW), (size_t)kernel_dyn_lds_bytes(e),
+                     stream, a);
   if (hipGetLastError() != hipSuccess) return FA_ERR_LAUNCH;
   if (splits > 1) {
     MergeArgs m;

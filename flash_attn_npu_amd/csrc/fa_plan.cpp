@@ -50,15 +50,25 @@ struct KernelMeta {
   bool splittable;    // supports split-KV (partial outputs + merge)
 };
 
-// LDS bytes of one workgroup (what the kernels' __shared__ arrays add up to;
-// fa_fwd.hip checks every entry against its kernel's own layout).
+// Dynamic LDS bytes of one workgroup: the Q area of the kernels with one
+// workgroup per CU, 16-bit V and fewer 1 KB DMA chunks per wave than 32 Q rows
+// fill (BLOCK_M rows of 2 D bytes); 0 for the others.
+constexpr int32_t kernel_dyn_lds_bytes(const KernelMeta &m) {
+  if (m.kind == kPingPong || m.wg_per_cu != 1 || v_is_fp8(m.dtype)) return 0;
+  const int32_t ndma = 2 * (m.BN * 2 * m.D / 1024 / m.NW);  // K and V chunks per wave and tile
+  return ndma < m.D / 16 ? 32 * m.NW * 2 * m.D : 0;
+}
+
+// LDS bytes of one workgroup (what the kernels' __shared__ arrays and the
+// dynamic Q area add up to; fa_fwd.hip checks every entry against its
+// kernel's own layout).
 constexpr int32_t kernel_lds_bytes(const KernelMeta &m) {
   if (m.kind == kPingPong) return 2 * m.stages * m.BN * 2 * m.D;  // K and V rings
   const int32_t k_tile = m.BN * 2 * m.D;
   const int32_t v_tile = m.BN * (v_is_fp8(m.dtype) ? 1 : 2) * m.D;
   const int32_t v_ipt = v_tile / 1024;  // 1 KB DMA instructions per V tile
   const int32_t v_ipw = v_ipt >= m.NW ? v_ipt / m.NW : 1;
-  return m.stages * (k_tile + v_ipw * m.NW * 1024);
+  return m.stages * (k_tile + v_ipw * m.NW * 1024) + kernel_dyn_lds_bytes(m);
 }
 
 constexpr KernelMeta dma(int D, int BN, int occ, int dtype, int causal) {
