@@ -155,7 +155,11 @@ def test_validate_fp8_v(lib):
     assert lib.fa_query_config(ctypes.byref(_params(shape=(1, 2, 4096, 256), dtype=3)), out) == 0
     assert out[1] == 64 and out[5] == 2 * (64 * 512 + 64 * 256)
     assert lib.fa_query_config(ctypes.byref(_params(shape=(1, 2, 4096, 256), dtype=1)), out) == 0
-    assert out[1] == 32
+    # 16-bit V: two 32-key K + V stages and the 64 KB Q area of 128 whole rows.
+    assert out[1] == 32 and out[5] == 2 * (32 * 512 + 32 * 512) + 128 * 512
+    # 64-key D = 256 tiles hold the Q rows in the wave's own DMA chunks: no Q area.
+    assert lib.fa_query_config(ctypes.byref(_params(shape=(1, 2, 4096, 256), dtype=1, bm=128, bn=64)), out) == 0
+    assert out[1] == 64 and out[5] == 2 * (64 * 512 + 64 * 512)
 
 
 def test_validate_rejects_slices_over_2gib(lib):
