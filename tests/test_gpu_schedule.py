@@ -42,9 +42,11 @@ def test_launch_slots_wrap(fa):
     torch.cuda.synchronize()
 
 
-def test_graph_replays(fa):
-    """A captured launch replays with fresh queues (the last user resets them)."""
-    q, k, v = _inputs(23, (2, 4, 700, 128))
+@pytest.mark.parametrize("shape", [(2, 4, 700, 128), (1, 4, 700, 256)])
+def test_graph_replays(fa, shape):
+    """A captured launch replays with fresh queues (the last user resets them).
+    D = 256 takes the kernel whose Q area is the launch's dynamic LDS."""
+    q, k, v = _inputs(23, shape)
     want_o, want_l = fa.attention(q, k, v, True, 0.1, return_lse=True)
     torch.cuda.synchronize()
     s = torch.cuda.Stream()
